@@ -1,0 +1,228 @@
+/*
+ * mvlm_hip.h — C ABI of the MI355X (gfx950) matmul hot path of MVLM.
+ *
+ * Plain C: opaque handles, pointers and sizes; no HIP, OpenCL or C++ types.
+ * Every function returns an int status (MVLM_OK == 0, negative on error); on
+ * error it also prints the message to stderr (as the reference's CL_CHECK_NULL
+ * does, src/engine/compute.cpp:12-17) and keeps it for mvlm_last_error().
+ *
+ * Layout contract.  Packed weights are built from either
+ *   - MVLM_LAYOUT_NK: GGUF-native [N rows][K], K contiguous (y = x * W^T), or
+ *   - MVLM_LAYOUT_KN: the reference's create_weight_image input, [K rows][N]
+ *     (src/engine/memory.cpp:28-79, rows = K, cols = N),
+ * and always hold the weight as [N][K] in HBM.  Quantized weights (Q8_0, Q4_0)
+ * are accepted only as GGUF blocks along K (MVLM_LAYOUT_NK, K % 32 == 0).
+ *
+ * Threading.  One in-order HIP stream per device handle, default priority.
+ * Calls on one handle are not thread-safe (as the reference's single in-order
+ * queue, src/engine/device.cpp:298-300).  Launch functions only enqueue; an
+ * mvlm_event** argument may be NULL, otherwise the caller owns the returned
+ * event and releases it with mvlm_event_release (src/engine/compute.cpp
+ * returns a cl_event the caller must wait on and release).
+ */
+#ifndef MVLM_HIP_H
+#define MVLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MVLM_ABI_VERSION 1
+
+/* ---- status codes ------------------------------------------------------- */
+enum mvlm_status {
+    MVLM_OK = 0,
+    MVLM_ERR_INVALID_ARG = -1,   /* null handle, bad size, bad dtype/layout  */
+    MVLM_ERR_NO_DEVICE = -2,     /* no HIP device, or ordinal out of range   */
+    MVLM_ERR_OUT_OF_MEMORY = -3, /* device or host allocation failed        */
+    MVLM_ERR_HIP = -4,           /* a HIP runtime call failed               */
+    MVLM_ERR_UNSUPPORTED = -5,   /* valid request this build does not serve */
+    MVLM_ERR_BUFFER_TOO_SMALL = -6
+};
+
+/* ---- element types (ggml type ids, src/models/gguf_loader.h:12-31) ----- */
+enum mvlm_dtype {
+    MVLM_F32 = 0,
+    MVLM_F16 = 1,
+    MVLM_Q4_0 = 2,
+    MVLM_Q8_0 = 8,
+    MVLM_BF16 = 30
+};
+
+enum mvlm_layout { MVLM_LAYOUT_NK = 0, MVLM_LAYOUT_KN = 1 };
+
+typedef struct mvlm_device mvlm_device;
+typedef struct mvlm_buffer mvlm_buffer;
+typedef struct mvlm_weight mvlm_weight;
+typedef struct mvlm_event mvlm_event;
+typedef struct mvlm_pool mvlm_pool;
+
+/* Mirrors the fields of the reference's DeviceInfo that make sense on HIP
+ * (src/engine/device.h:13-55) plus the peaks used for roofline fractions. */
+typedef struct mvlm_device_info {
+    char device_name[256];
+    char arch_name[64];              /* e.g. "gfx950:sramecc+:xnack-" */
+    int ordinal;
+    int compute_units;
+    int max_clock_mhz;
+    int memory_clock_mhz;
+    int memory_bus_width_bits;
+    int wavefront_size;
+    uint64_t global_mem_size;
+    uint64_t local_mem_size;         /* LDS bytes per work-group */
+    uint64_t l2_cache_size;
+    double peak_hbm_gbs;             /* nominal MI355X HBM3E: 8000 GB/s */
+    double peak_fp16_tflops;         /* nominal dense fp16/bf16 MFMA: 2500 */
+} mvlm_device_info;
+
+/* ---- errors -------------------------------------------------------------- */
+/* Message of the last failing call on this thread ("" if none). */
+const char* mvlm_last_error(void);
+int mvlm_abi_version(void);
+
+/* ---- device lifecycle (src/engine/device.h:58-75) ------------------------ */
+int mvlm_device_count(int* count);
+/* replaces init_device (device.cpp:141-304); no program build step: the
+ * gfx950 code objects are part of this library. */
+int mvlm_device_create(int ordinal, mvlm_device** out);
+int mvlm_device_destroy(mvlm_device* dev);                      /* destroy_device */
+int mvlm_device_get_info(const mvlm_device* dev, mvlm_device_info* info);
+int mvlm_device_synchronize(mvlm_device* dev);                  /* clFinish */
+
+/* ---- buffers (src/engine/memory.h:15-35) ---------------------------------- */
+/* create_buffer (memory.cpp:81-89): device allocation of `bytes`. */
+int mvlm_buffer_alloc(mvlm_device* dev, size_t bytes, mvlm_buffer** out);
+/* A view of [offset, offset+bytes) of `parent` (the reference makes a
+ * sub-buffer for the last row before the LM head, moondream2.cpp:528-536).
+ * The view must be freed before its parent. */
+int mvlm_buffer_view(mvlm_buffer* parent, size_t offset, size_t bytes, mvlm_buffer** out);
+int mvlm_buffer_free(mvlm_buffer* buf);
+size_t mvlm_buffer_size(const mvlm_buffer* buf);
+/* Synchronous host<->device copies on the device stream. */
+int mvlm_buffer_upload(mvlm_buffer* buf, size_t offset, const void* src, size_t bytes);
+int mvlm_buffer_download(const mvlm_buffer* buf, size_t offset, void* dst, size_t bytes);
+int mvlm_buffer_fill_zero(mvlm_buffer* buf);
+
+/* BufferPool ping-pong (memory.h:25-35, memory.cpp:113-157). */
+int mvlm_pool_init(mvlm_device* dev, size_t bytes, mvlm_pool** out);   /* init_buffer_pool */
+mvlm_buffer* mvlm_pool_current(mvlm_pool* pool);                       /* get_current_buffer */
+mvlm_buffer* mvlm_pool_next(mvlm_pool* pool);                          /* get_next_buffer */
+int mvlm_pool_swap(mvlm_pool* pool);                                   /* swap_buffers */
+int mvlm_pool_destroy(mvlm_pool* pool);                                /* destroy_buffer_pool */
+
+/* ---- packed weights (replaces create_weight_image, memory.cpp:28-79) ---- */
+/* `src` is host memory: for F32/F16/BF16 N*K elements in `layout`; for Q8_0 /
+ * Q4_0 N*(K/32) GGUF blocks (34 / 18 bytes) in MVLM_LAYOUT_NK. */
+int mvlm_weight_pack(mvlm_device* dev, const void* src, int dtype, int layout,
+                     int N, int K, mvlm_weight** out);
+/* Same, from GGUF-layout bytes already in device memory (no host staging). */
+int mvlm_weight_pack_device(mvlm_device* dev, const mvlm_buffer* src, int dtype, int layout,
+                            int N, int K, mvlm_weight** out);
+int mvlm_weight_free(mvlm_weight* w);
+int mvlm_weight_dtype(const mvlm_weight* w);
+int mvlm_weight_shape(const mvlm_weight* w, int* N, int* K);
+/* Bytes the weight occupies in HBM (codes + scales + padding). */
+size_t mvlm_weight_bytes(const mvlm_weight* w);
+/* Writes the exact fp32 values of the packed weight as [N][K] row-major into
+ * `out` (N*K*4 bytes): d*q for Q8_0, (q-8)*d for Q4_0. */
+int mvlm_weight_dequant(mvlm_device* dev, const mvlm_weight* w, mvlm_buffer* out, mvlm_event** ev);
+
+/* ---- reference GEMM entry points (src/engine/compute.h:13-33) ------------ */
+/* C[M,N] = A[M,K] * B[K,N]; A, B, C fp16 row-major, fp32 accumulation in
+ * ascending k with fused multiply-add, round-to-nearest-even fp16 store: the
+ * arithmetic of gemm_naive (gemm.cl:26-51).  dispatch_gemm_naive. */
+int mvlm_gemm_naive(mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer* B,
+                    mvlm_buffer* C, int M, int N, int K, mvlm_event** ev);
+/* Same arithmetic as gemm_tiled (gemm.cl:74-136), LDS-tiled; bit-identical
+ * to mvlm_gemm_naive.  dispatch_gemm_tiled. */
+int mvlm_gemm_tiled(mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer* B,
+                    mvlm_buffer* C, int M, int N, int K, mvlm_event** ev);
+/* dispatch_gemm_image (compute.cpp:90-120): C[M,N] = A[M,K] * W, W a packed
+ * weight (F16 or BF16), computed on MFMA with fp32 accumulation.  a_dtype is
+ * F16 or BF16 (matching W), c_dtype F32, F16 or BF16. */
+int mvlm_gemm_packed(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, const mvlm_weight* W,
+                     mvlm_buffer* C, int c_dtype, int M, int N, int K, mvlm_event** ev);
+/* dispatch_gemv (compute.cpp:122-152): y[N] = x[K] * W.  W packed F32, F16,
+ * BF16, Q8_0 or Q4_0; x_dtype F32, F16 or BF16 (F32 for quantized W);
+ * y_dtype F32, F16 or BF16.  fp32 accumulation. */
+int mvlm_gemv(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W,
+              mvlm_buffer* y, int y_dtype, int N, int K, mvlm_event** ev);
+
+/* ---- dequantizing GEMV / skinny GEMM (planned in README.md:57, PLAN.md:65) */
+/* y[N] = x[K] * W^T, W packed Q8_0, x and y fp32. */
+int mvlm_gemv_q8_0(mvlm_device* dev, const mvlm_buffer* x, const mvlm_weight* W,
+                   mvlm_buffer* y, int N, int K, mvlm_event** ev);
+int mvlm_gemv_q4_0(mvlm_device* dev, const mvlm_buffer* x, const mvlm_weight* W,
+                   mvlm_buffer* y, int N, int K, mvlm_event** ev);
+/* Y[M,N] = X[M,K] * W^T for 1 <= M <= 16, X and Y fp32 row-major. */
+int mvlm_gemm_q8_0(mvlm_device* dev, const mvlm_buffer* X, const mvlm_weight* W,
+                   mvlm_buffer* Y, int M, int N, int K, mvlm_event** ev);
+int mvlm_gemm_q4_0(mvlm_device* dev, const mvlm_buffer* X, const mvlm_weight* W,
+                   mvlm_buffer* Y, int M, int N, int K, mvlm_event** ev);
+
+/* ---- batched NT GEMM (the Q*K^T of attention.cl:84-88, all heads at once) */
+/* C[b][m][n] = sum_k A[b][m][k] * B[b][n][k]; A, B fp16, C fp32; leading
+ * dimensions and batch strides in elements. */
+int mvlm_gemm_batched(mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer* B,
+                      mvlm_buffer* C, int batch, int M, int N, int K,
+                      int64_t lda, int64_t ldb, int64_t ldc,
+                      int64_t strideA, int64_t strideB, int64_t strideC, mvlm_event** ev);
+
+/* ---- synthetic inputs on the device ------------------------------------- */
+/* SplitMix64 -> Box-Muller fills (same generator as the CPU oracle, computed
+ * on the GPU so multi-GB weight sets need no host staging). */
+int mvlm_fill_normal(mvlm_device* dev, mvlm_buffer* buf, int dtype, size_t count,
+                     uint64_t seed, double stddev);
+/* Random GGUF-distributed quantized weight, packed directly:
+ * Q8_0 qs uniform in [-127,127], d = f16(|N(0,wstd)|/127);
+ * Q4_0 codes uniform in [0,15],  d = f16(|N(0,wstd)|/8). */
+int mvlm_weight_random(mvlm_device* dev, int dtype, int N, int K, uint64_t seed,
+                       double wstd, mvlm_weight** out);
+
+/* ---- events (src/engine/profiler.cpp:25-54 reads START/END of a cl_event) */
+int mvlm_event_wait(mvlm_event* ev);
+/* Device time between the launch's start and end markers, in ms. */
+int mvlm_event_elapsed_ms(mvlm_event* ev, float* ms);
+int mvlm_event_release(mvlm_event* ev);
+
+/* ---- plans: a recorded sequence of launches -------------------------------
+ * The decode-step driver.  The reference issues one dispatch per projection
+ * and blocks on each event (src/models/moondream2.cpp:359-541, e.g. :379);
+ * its "recordable queue" replay is an empty stub (src/engine/pipeline.cpp:45-125).
+ * A plan records the launches once (validated at add time, like the direct
+ * entry points), then enqueues them from native code, optionally replaying a
+ * captured HIP graph.  Buffers and weights a plan names must outlive it. */
+typedef struct mvlm_plan mvlm_plan;
+int mvlm_plan_create(mvlm_device* dev, mvlm_plan** out);
+int mvlm_plan_destroy(mvlm_plan* plan);
+int mvlm_plan_size(const mvlm_plan* plan);
+/* Y[M,N] = X[M,K] * W^T with N, K taken from W: dense W needs M == 1
+ * (mvlm_gemv); Q8_0 / Q4_0 W takes 1 <= M <= 16 (mvlm_gemm_q8_0/q4_0). */
+int mvlm_plan_add_gemv(mvlm_plan* plan, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W,
+                       mvlm_buffer* y, int y_dtype, int M);
+int mvlm_plan_add_gemm_packed(mvlm_plan* plan, const mvlm_buffer* A, int a_dtype, const mvlm_weight* W,
+                              mvlm_buffer* C, int c_dtype, int M);
+int mvlm_plan_add_gemm_batched(mvlm_plan* plan, const mvlm_buffer* A, const mvlm_buffer* B,
+                               mvlm_buffer* C, int batch, int M, int N, int K,
+                               int64_t lda, int64_t ldb, int64_t ldc,
+                               int64_t strideA, int64_t strideB, int64_t strideC);
+/* enable != 0: capture the plan into a HIP graph (now) and replay it on run. */
+int mvlm_plan_use_graph(mvlm_plan* plan, int enable);
+/* Enqueue the plan `repeats` times; `ev` (optional) spans everything enqueued. */
+int mvlm_plan_run(mvlm_plan* plan, int repeats, mvlm_event** ev);
+/* One eager run with a marker between launches: op_ms[i] is the device time
+ * from the end of launch i-1 (the start, for i == 0) to the end of launch i. */
+int mvlm_plan_profile(mvlm_plan* plan, float* op_ms, int capacity);
+
+/* ---- stream markers for host-side timing of a region ---------------------- */
+/* Records a marker on the device stream; elapsed time between two markers. */
+int mvlm_marker_record(mvlm_device* dev, mvlm_event** out);
+int mvlm_marker_elapsed_ms(mvlm_event* start, mvlm_event* end, float* ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,120 @@
+// Internal definitions shared by the host runtime and the kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bf16.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/mvlm_hip.h"
+
+struct mvlm_device {
+    int ordinal = 0;
+    hipStream_t stream = nullptr;
+    hipDeviceProp_t prop{};
+};
+
+struct mvlm_buffer {
+    mvlm_device* dev = nullptr;
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    bool owned = false;        // false for views
+    mvlm_buffer* parent = nullptr;
+    int views = 0;             // live views of this buffer
+};
+
+// HBM layout of a packed weight, always [N][K] with K contiguous:
+//  dense (F32/F16/BF16): data = [N][ld] elements, ld = K rounded up to 64,
+//                        columns K..ld-1 zero.
+//  Q8_0: data = int8 codes [N][K] (row stride K bytes);
+//        scales = fp16 d [N][K/32].
+//  Q4_0: data = nibble codes [N][K/2] (row stride K/2 bytes); each block of
+//        32 weights is 16 bytes where byte j holds weight j in its low nibble
+//        and weight j+16 in its high nibble (the GGUF order);
+//        scales = fp16 d [N][K/32].
+struct mvlm_weight {
+    mvlm_device* dev = nullptr;
+    int dtype = 0;
+    int N = 0, K = 0;
+    int64_t ld = 0;            // dense: elements per row; quant: code bytes per row
+    void* data = nullptr;
+    void* scales = nullptr;
+    void* alloc = nullptr;     // single allocation holding data (+ scales)
+    size_t bytes = 0;
+};
+
+struct mvlm_event {
+    mvlm_device* dev = nullptr;
+    hipEvent_t start = nullptr;
+    hipEvent_t end = nullptr;
+};
+
+struct mvlm_pool {
+    mvlm_buffer* buffers[2] = {nullptr, nullptr};
+    size_t size = 0;
+    int current = 0;
+};
+
+namespace mvlm {
+
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int check_hip(hipError_t e, const char* what);
+
+#define REQUIRE(cond, ...)                                                      \
+    do {                                                                        \
+        if (!(cond)) return ::mvlm::set_error(MVLM_ERR_INVALID_ARG, __VA_ARGS__); \
+    } while (0)
+
+#define HIP_TRY(expr)                                     \
+    do {                                                  \
+        int _st = ::mvlm::check_hip((expr), #expr);       \
+        if (_st != MVLM_OK) return _st;                   \
+    } while (0)
+
+inline size_t dtype_size(int dt) {
+    switch (dt) {
+        case MVLM_F32: return 4;
+        case MVLM_F16: case MVLM_BF16: return 2;
+        default: return 0;
+    }
+}
+inline bool is_dense(int dt) { return dt == MVLM_F32 || dt == MVLM_F16 || dt == MVLM_BF16; }
+inline bool is_quant(int dt) { return dt == MVLM_Q8_0 || dt == MVLM_Q4_0; }
+inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+// Launch bracketing: records the start marker when the caller asked for an
+// event, and finishes (end marker + hand-over) after the launch.
+struct LaunchScope {
+    mvlm_device* dev;
+    mvlm_event** out;
+    mvlm_event* ev = nullptr;
+    int status = MVLM_OK;
+    LaunchScope(mvlm_device* d, mvlm_event** o);
+    int finish(const char* kernel_name);
+};
+
+// Kernel launchers (defined in the .hip files).  They assume validated input.
+hipError_t launch_gemm_naive(hipStream_t s, const uint16_t* A, const uint16_t* B, uint16_t* C,
+                             int M, int N, int K);
+hipError_t launch_gemm_tiled(hipStream_t s, const uint16_t* A, const uint16_t* B, uint16_t* C,
+                             int M, int N, int K);
+hipError_t launch_gemv_dense(hipStream_t s, const void* x, int x_dtype, const mvlm_weight* W,
+                             void* y, int y_dtype, int N, int K);
+hipError_t launch_gemv_quant(hipStream_t s, const float* X, const mvlm_weight* W, float* Y,
+                             int M, int N, int K);
+hipError_t launch_gemm_mfma(hipStream_t s, const void* A, int ab_dtype, const void* B, void* C,
+                            int c_dtype, int batch, int M, int N, int K, int64_t lda, int64_t ldb,
+                            int64_t ldc, int64_t strideA, int64_t strideB, int64_t strideC,
+                            int num_cus);
+hipError_t launch_pack(hipStream_t s, const void* src, int dtype, int layout, int N, int K,
+                       mvlm_weight* w);
+hipError_t launch_dequant(hipStream_t s, const mvlm_weight* w, float* out);
+hipError_t launch_fill_normal(hipStream_t s, void* dst, int dtype, size_t count, uint64_t seed,
+                              double stddev);
+hipError_t launch_weight_random(hipStream_t s, mvlm_weight* w, uint64_t seed, double wstd);
+
+}  // namespace mvlm

@@ -1,0 +1,369 @@
+// Launch entry points and plans.
+//
+// Every launch is first turned into a validated Op (all checks on the host,
+// before anything is enqueued), then enqueued by enqueue_op.  The direct
+// entry points (mvlm_gemm_*, mvlm_gemv*) do both at once, matching the
+// reference dispatchers (src/engine/compute.cpp:28-152); a plan validates at
+// add time and enqueues from native code on every run, eagerly or by
+// replaying a captured HIP graph.
+#include "common.h"
+
+#include <new>
+#include <vector>
+
+using namespace mvlm;
+
+namespace {
+
+enum OpKind { OP_GEMM_NAIVE, OP_GEMM_TILED, OP_GEMM_MFMA, OP_GEMV_DENSE, OP_GEMV_QUANT };
+
+struct Op {
+    OpKind kind;
+    const void* a = nullptr;      // A / x / X
+    const void* b = nullptr;      // B (naive, tiled, batched)
+    void* c = nullptr;            // C / y / Y
+    const mvlm_weight* w = nullptr;
+    int a_dtype = MVLM_F16, c_dtype = MVLM_F32;
+    int batch = 1, M = 0, N = 0, K = 0;
+    int64_t lda = 0, ldb = 0, ldc = 0, sA = 0, sB = 0, sC = 0;
+    int num_cus = 256;
+};
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int need(const mvlm_buffer* b, size_t bytes, const char* fn, const char* name) {
+    if (b->bytes < bytes)
+        return set_error(MVLM_ERR_BUFFER_TOO_SMALL, "%s: %s holds %zu bytes, %zu needed", fn, name, b->bytes, bytes);
+    return MVLM_OK;
+}
+
+#define NEED(buf, bytes, name)                                   \
+    do {                                                         \
+        int _st = need((buf), (bytes), fn, (name));              \
+        if (_st != MVLM_OK) return _st;                          \
+    } while (0)
+
+int make_ref_gemm(OpKind kind, mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer* B, mvlm_buffer* C,
+                  int M, int N, int K, const char* fn, Op* op) {
+    REQUIRE(dev && A && B && C, "%s: null argument", fn);
+    REQUIRE(A->dev == dev && B->dev == dev && C->dev == dev, "%s: buffers belong to another device", fn);
+    REQUIRE(M > 0 && N > 0 && K > 0, "%s: M=%d N=%d K=%d must be positive", fn, M, N, K);
+    NEED(A, (size_t)M * K * 2, "A");
+    NEED(B, (size_t)K * N * 2, "B");
+    NEED(C, (size_t)M * N * 2, "C");
+    op->kind = kind;
+    op->a = A->ptr; op->b = B->ptr; op->c = C->ptr;
+    op->M = M; op->N = N; op->K = K;
+    return MVLM_OK;
+}
+
+int make_gemm_packed(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, const mvlm_weight* W, mvlm_buffer* C,
+                     int c_dtype, int M, int N, int K, const char* fn, Op* op) {
+    REQUIRE(dev && A && W && C, "%s: null argument", fn);
+    REQUIRE(A->dev == dev && W->dev == dev && C->dev == dev, "%s: handles belong to another device", fn);
+    REQUIRE(M > 0 && N > 0 && K > 0, "%s: M=%d N=%d K=%d must be positive", fn, M, N, K);
+    REQUIRE(W->N == N && W->K == K, "%s: weight is [%d x %d], call asks for N=%d K=%d", fn, W->N, W->K, N, K);
+    REQUIRE(W->dtype == MVLM_F16 || W->dtype == MVLM_BF16, "%s: weight dtype %d is not F16/BF16", fn, W->dtype);
+    REQUIRE(a_dtype == W->dtype, "%s: activation dtype %d differs from weight dtype %d", fn, a_dtype, W->dtype);
+    REQUIRE(is_dense(c_dtype), "%s: output dtype %d is not F32/F16/BF16", fn, c_dtype);
+    if (K % 8 != 0) return set_error(MVLM_ERR_UNSUPPORTED, "%s: K=%d is not a multiple of 8 (16-byte rows)", fn, K);
+    REQUIRE(aligned16(A->ptr) && aligned16(C->ptr), "%s: A and C must be 16-byte aligned", fn);
+    NEED(A, (size_t)M * K * 2, "A");
+    NEED(C, (size_t)M * N * dtype_size(c_dtype), "C");
+    op->kind = OP_GEMM_MFMA;
+    op->a = A->ptr; op->b = W->data; op->c = C->ptr; op->w = W;
+    op->a_dtype = a_dtype; op->c_dtype = c_dtype;
+    op->M = M; op->N = N; op->K = K;
+    op->lda = K; op->ldb = W->ld; op->ldc = N;
+    op->num_cus = dev->prop.multiProcessorCount;
+    return MVLM_OK;
+}
+
+int make_gemm_batched(mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer* B, mvlm_buffer* C, int batch,
+                      int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc, int64_t sA, int64_t sB,
+                      int64_t sC, const char* fn, Op* op) {
+    REQUIRE(dev && A && B && C, "%s: null argument", fn);
+    REQUIRE(A->dev == dev && B->dev == dev && C->dev == dev, "%s: buffers belong to another device", fn);
+    REQUIRE(batch > 0 && M > 0 && N > 0 && K > 0, "%s: batch=%d M=%d N=%d K=%d must be positive", fn, batch, M, N, K);
+    REQUIRE(lda >= K && ldb >= K && ldc >= N, "%s: leading dimensions too small", fn);
+    REQUIRE(sA >= 0 && sB >= 0 && sC >= 0, "%s: negative batch stride", fn);
+    if (K % 8 != 0 || lda % 8 != 0 || ldb % 8 != 0 || sA % 8 != 0 || sB % 8 != 0)
+        return set_error(MVLM_ERR_UNSUPPORTED, "%s: K, lda, ldb and the A/B strides must be multiples of 8", fn);
+    REQUIRE(aligned16(A->ptr) && aligned16(B->ptr) && ((uintptr_t)C->ptr & 3u) == 0,
+            "%s: A and B must be 16-byte aligned, C 4-byte aligned", fn);
+    NEED(A, ((size_t)(batch - 1) * sA + (size_t)(M - 1) * lda + K) * 2, "A");
+    NEED(B, ((size_t)(batch - 1) * sB + (size_t)(N - 1) * ldb + K) * 2, "B");
+    NEED(C, ((size_t)(batch - 1) * sC + (size_t)(M - 1) * ldc + N) * 4, "C");
+    op->kind = OP_GEMM_MFMA;
+    op->a = A->ptr; op->b = B->ptr; op->c = C->ptr;
+    op->a_dtype = MVLM_F16; op->c_dtype = MVLM_F32;
+    op->batch = batch; op->M = M; op->N = N; op->K = K;
+    op->lda = lda; op->ldb = ldb; op->ldc = ldc; op->sA = sA; op->sB = sB; op->sC = sC;
+    op->num_cus = dev->prop.multiProcessorCount;
+    return MVLM_OK;
+}
+
+// Dense GEMV (M == 1) or dequantizing GEMV / skinny GEMM (M <= 16).
+// want_dtype: required weight dtype, or -1 for any.
+int make_gemv(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W, mvlm_buffer* y,
+              int y_dtype, int M, int N, int K, int want_dtype, const char* fn, Op* op) {
+    REQUIRE(dev && x && W && y, "%s: null argument", fn);
+    REQUIRE(x->dev == dev && W->dev == dev && y->dev == dev, "%s: handles belong to another device", fn);
+    if (want_dtype >= 0) REQUIRE(W->dtype == want_dtype, "%s: weight dtype %d, expected %d", fn, W->dtype, want_dtype);
+    REQUIRE(N > 0 && K > 0, "%s: N=%d K=%d must be positive", fn, N, K);
+    REQUIRE(W->N == N && W->K == K, "%s: weight is [%d x %d], call asks for N=%d K=%d", fn, W->N, W->K, N, K);
+    REQUIRE(aligned16(x->ptr), "%s: x must be 16-byte aligned", fn);
+    op->a = x->ptr; op->c = y->ptr; op->w = W;
+    op->M = M; op->N = N; op->K = K;
+    op->a_dtype = x_dtype; op->c_dtype = y_dtype;
+    if (is_quant(W->dtype)) {
+        REQUIRE(M >= 1 && M <= 16, "%s: M=%d outside [1, 16]", fn, M);
+        REQUIRE(x_dtype == MVLM_F32 && y_dtype == MVLM_F32, "%s: quantized weights take fp32 x and y", fn);
+        NEED(x, (size_t)M * K * 4, "x");
+        NEED(y, (size_t)M * N * 4, "y");
+        op->kind = OP_GEMV_QUANT;
+        return MVLM_OK;
+    }
+    REQUIRE(M == 1, "%s: dense weights take M == 1 (M=%d); use mvlm_gemm_packed", fn, M);
+    REQUIRE(is_dense(x_dtype) && is_dense(y_dtype), "%s: x/y dtypes must be F32/F16/BF16", fn);
+    NEED(x, (size_t)K * dtype_size(x_dtype), "x");
+    NEED(y, (size_t)N * dtype_size(y_dtype), "y");
+    op->kind = OP_GEMV_DENSE;
+    return MVLM_OK;
+}
+
+hipError_t enqueue_op(hipStream_t s, const Op& op) {
+    switch (op.kind) {
+        case OP_GEMM_NAIVE:
+            return launch_gemm_naive(s, (const uint16_t*)op.a, (const uint16_t*)op.b, (uint16_t*)op.c, op.M, op.N, op.K);
+        case OP_GEMM_TILED:
+            return launch_gemm_tiled(s, (const uint16_t*)op.a, (const uint16_t*)op.b, (uint16_t*)op.c, op.M, op.N, op.K);
+        case OP_GEMM_MFMA:
+            return launch_gemm_mfma(s, op.a, op.a_dtype, op.b, op.c, op.c_dtype, op.batch, op.M, op.N, op.K,
+                                    op.lda, op.ldb, op.ldc, op.sA, op.sB, op.sC, op.num_cus);
+        case OP_GEMV_DENSE:
+            return launch_gemv_dense(s, op.a, op.a_dtype, op.w, op.c, op.c_dtype, op.N, op.K);
+        case OP_GEMV_QUANT:
+            return launch_gemv_quant(s, (const float*)op.a, op.w, (float*)op.c, op.M, op.N, op.K);
+    }
+    return hipErrorInvalidValue;
+}
+
+int run_one(mvlm_device* dev, const Op& op, mvlm_event** ev, const char* fn) {
+    LaunchScope ls(dev, ev);
+    if (ls.status != MVLM_OK) return ls.status;
+    hipError_t e = enqueue_op(dev->stream, op);
+    if (e != hipSuccess) ls.status = check_hip(e, fn);
+    return ls.finish(fn);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// direct entry points
+// ---------------------------------------------------------------------------
+
+#define RUN(make_call)                                 \
+    do {                                               \
+        if (ev) *ev = nullptr;                         \
+        Op op{};                                       \
+        int st = (make_call);                          \
+        if (st != MVLM_OK) return st;                  \
+        return run_one(dev, op, ev, fn);               \
+    } while (0)
+
+extern "C" int mvlm_gemm_naive(mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer* B, mvlm_buffer* C,
+                               int M, int N, int K, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(make_ref_gemm(OP_GEMM_NAIVE, dev, A, B, C, M, N, K, fn, &op));
+}
+
+extern "C" int mvlm_gemm_tiled(mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer* B, mvlm_buffer* C,
+                               int M, int N, int K, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(make_ref_gemm(OP_GEMM_TILED, dev, A, B, C, M, N, K, fn, &op));
+}
+
+extern "C" int mvlm_gemm_packed(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, const mvlm_weight* W,
+                                mvlm_buffer* C, int c_dtype, int M, int N, int K, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(make_gemm_packed(dev, A, a_dtype, W, C, c_dtype, M, N, K, fn, &op));
+}
+
+extern "C" int mvlm_gemm_batched(mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer* B, mvlm_buffer* C,
+                                 int batch, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
+                                 int64_t strideA, int64_t strideB, int64_t strideC, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(make_gemm_batched(dev, A, B, C, batch, M, N, K, lda, ldb, ldc, strideA, strideB, strideC, fn, &op));
+}
+
+extern "C" int mvlm_gemv(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W,
+                         mvlm_buffer* y, int y_dtype, int N, int K, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(make_gemv(dev, x, x_dtype, W, y, y_dtype, 1, N, K, -1, fn, &op));
+}
+
+extern "C" int mvlm_gemv_q8_0(mvlm_device* dev, const mvlm_buffer* x, const mvlm_weight* W, mvlm_buffer* y,
+                              int N, int K, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(make_gemv(dev, x, MVLM_F32, W, y, MVLM_F32, 1, N, K, MVLM_Q8_0, fn, &op));
+}
+
+extern "C" int mvlm_gemv_q4_0(mvlm_device* dev, const mvlm_buffer* x, const mvlm_weight* W, mvlm_buffer* y,
+                              int N, int K, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(make_gemv(dev, x, MVLM_F32, W, y, MVLM_F32, 1, N, K, MVLM_Q4_0, fn, &op));
+}
+
+extern "C" int mvlm_gemm_q8_0(mvlm_device* dev, const mvlm_buffer* X, const mvlm_weight* W, mvlm_buffer* Y,
+                              int M, int N, int K, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(make_gemv(dev, X, MVLM_F32, W, Y, MVLM_F32, M, N, K, MVLM_Q8_0, fn, &op));
+}
+
+extern "C" int mvlm_gemm_q4_0(mvlm_device* dev, const mvlm_buffer* X, const mvlm_weight* W, mvlm_buffer* Y,
+                              int M, int N, int K, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(make_gemv(dev, X, MVLM_F32, W, Y, MVLM_F32, M, N, K, MVLM_Q4_0, fn, &op));
+}
+
+// ---------------------------------------------------------------------------
+// plans
+// ---------------------------------------------------------------------------
+
+struct mvlm_plan {
+    mvlm_device* dev = nullptr;
+    std::vector<Op> ops;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+static void drop_graph(mvlm_plan* p) {
+    if (p->exec) (void)hipGraphExecDestroy(p->exec);
+    if (p->graph) (void)hipGraphDestroy(p->graph);
+    p->exec = nullptr;
+    p->graph = nullptr;
+}
+
+extern "C" int mvlm_plan_create(mvlm_device* dev, mvlm_plan** out) {
+    REQUIRE(dev && out, "mvlm_plan_create: null argument");
+    *out = nullptr;
+    mvlm_plan* p = new (std::nothrow) mvlm_plan();
+    if (!p) return set_error(MVLM_ERR_OUT_OF_MEMORY, "plan allocation failed");
+    p->dev = dev;
+    *out = p;
+    return MVLM_OK;
+}
+
+extern "C" int mvlm_plan_destroy(mvlm_plan* plan) {
+    REQUIRE(plan, "mvlm_plan_destroy: plan is null");
+    drop_graph(plan);
+    delete plan;
+    return MVLM_OK;
+}
+
+extern "C" int mvlm_plan_size(const mvlm_plan* plan) { return plan ? (int)plan->ops.size() : MVLM_ERR_INVALID_ARG; }
+
+static int plan_push(mvlm_plan* plan, const Op& op) {
+    drop_graph(plan);   // a recorded graph no longer matches
+    try {
+        plan->ops.push_back(op);
+    } catch (...) {
+        return set_error(MVLM_ERR_OUT_OF_MEMORY, "plan growth failed");
+    }
+    return MVLM_OK;
+}
+
+extern "C" int mvlm_plan_add_gemv(mvlm_plan* plan, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W,
+                                  mvlm_buffer* y, int y_dtype, int M) {
+    const char* fn = __func__;
+    REQUIRE(plan && W, "%s: null argument", fn);
+    Op op{};
+    int st = make_gemv(plan->dev, x, x_dtype, W, y, y_dtype, M, W->N, W->K, -1, fn, &op);
+    return st != MVLM_OK ? st : plan_push(plan, op);
+}
+
+extern "C" int mvlm_plan_add_gemm_packed(mvlm_plan* plan, const mvlm_buffer* A, int a_dtype, const mvlm_weight* W,
+                                         mvlm_buffer* C, int c_dtype, int M) {
+    const char* fn = __func__;
+    REQUIRE(plan && W, "%s: null argument", fn);
+    Op op{};
+    int st = make_gemm_packed(plan->dev, A, a_dtype, W, C, c_dtype, M, W->N, W->K, fn, &op);
+    return st != MVLM_OK ? st : plan_push(plan, op);
+}
+
+extern "C" int mvlm_plan_add_gemm_batched(mvlm_plan* plan, const mvlm_buffer* A, const mvlm_buffer* B,
+                                          mvlm_buffer* C, int batch, int M, int N, int K, int64_t lda,
+                                          int64_t ldb, int64_t ldc, int64_t strideA, int64_t strideB,
+                                          int64_t strideC) {
+    const char* fn = __func__;
+    REQUIRE(plan, "%s: null argument", fn);
+    Op op{};
+    int st = make_gemm_batched(plan->dev, A, B, C, batch, M, N, K, lda, ldb, ldc, strideA, strideB, strideC, fn, &op);
+    return st != MVLM_OK ? st : plan_push(plan, op);
+}
+
+static int enqueue_all(mvlm_plan* plan) {
+    for (const Op& op : plan->ops) {
+        hipError_t e = enqueue_op(plan->dev->stream, op);
+        if (e != hipSuccess) return check_hip(e, "plan launch");
+    }
+    return MVLM_OK;
+}
+
+extern "C" int mvlm_plan_use_graph(mvlm_plan* plan, int enable) {
+    REQUIRE(plan, "mvlm_plan_use_graph: plan is null");
+    drop_graph(plan);
+    if (!enable) return MVLM_OK;
+    REQUIRE(!plan->ops.empty(), "mvlm_plan_use_graph: the plan is empty");
+    hipStream_t s = plan->dev->stream;
+    HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    int st = enqueue_all(plan);
+    hipGraph_t g = nullptr;
+    int st2 = check_hip(hipStreamEndCapture(s, &g), "hipStreamEndCapture");
+    if (st == MVLM_OK) st = st2;
+    if (st != MVLM_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return st;
+    }
+    plan->graph = g;
+    st = check_hip(hipGraphInstantiate(&plan->exec, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+    if (st != MVLM_OK) drop_graph(plan);
+    return st;
+}
+
+extern "C" int mvlm_plan_run(mvlm_plan* plan, int repeats, mvlm_event** ev) {
+    if (ev) *ev = nullptr;
+    REQUIRE(plan, "mvlm_plan_run: plan is null");
+    REQUIRE(repeats >= 1, "mvlm_plan_run: repeats=%d must be positive", repeats);
+    LaunchScope ls(plan->dev, ev);
+    if (ls.status != MVLM_OK) return ls.status;
+    for (int r = 0; r < repeats && ls.status == MVLM_OK; ++r) {
+        if (plan->exec)
+            ls.status = check_hip(hipGraphLaunch(plan->exec, plan->dev->stream), "hipGraphLaunch");
+        else
+            ls.status = enqueue_all(plan);
+    }
+    return ls.finish("plan run");
+}
+
+extern "C" int mvlm_plan_profile(mvlm_plan* plan, float* op_ms, int capacity) {
+    REQUIRE(plan && op_ms, "mvlm_plan_profile: null argument");
+    const int n = (int)plan->ops.size();
+    REQUIRE(capacity >= n, "mvlm_plan_profile: capacity %d below the plan size %d", capacity, n);
+    std::vector<hipEvent_t> marks(n + 1, nullptr);
+    int st = MVLM_OK;
+    for (int i = 0; i <= n && st == MVLM_OK; ++i) st = check_hip(hipEventCreate(&marks[i]), "hipEventCreate");
+    hipStream_t s = plan->dev->stream;
+    if (st == MVLM_OK) st = check_hip(hipEventRecord(marks[0], s), "hipEventRecord");
+    for (int i = 0; i < n && st == MVLM_OK; ++i) {
+        hipError_t e = enqueue_op(s, plan->ops[i]);
+        st = (e == hipSuccess) ? check_hip(hipEventRecord(marks[i + 1], s), "hipEventRecord") : check_hip(e, "plan launch");
+    }
+    if (st == MVLM_OK) st = check_hip(hipEventSynchronize(marks[n]), "hipEventSynchronize");
+    for (int i = 0; i < n && st == MVLM_OK; ++i)
+        st = check_hip(hipEventElapsedTime(&op_ms[i], marks[i], marks[i + 1]), "hipEventElapsedTime");
+    for (hipEvent_t e : marks)
+        if (e) (void)hipEventDestroy(e);
+    return st;
+}

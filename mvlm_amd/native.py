@@ -1,0 +1,393 @@
+"""ctypes binding of libmvlm_hip.so (the C ABI declared in include/mvlm_hip.h).
+
+The Python side only moves buffers and calls the C ABI; every computation runs
+in the HIP library.  If the library has not been built, importing the binding
+raises instead of falling back to anything else.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, byref, c_char_p, c_double, c_float, c_int, c_int64, c_size_t, c_uint64, c_void_p
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "lib", "libmvlm_hip.so")
+
+F32, F16, Q4_0, Q8_0, BF16 = 0, 1, 2, 8, 30
+LAYOUT_NK, LAYOUT_KN = 0, 1
+DTYPE_SIZE = {F32: 4, F16: 2, BF16: 2}
+DTYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", Q8_0: "q8_0", Q4_0: "q4_0"}
+
+OK = 0
+ERR_INVALID_ARG, ERR_NO_DEVICE, ERR_OUT_OF_MEMORY, ERR_HIP, ERR_UNSUPPORTED, ERR_BUFFER_TOO_SMALL = -1, -2, -3, -4, -5, -6
+
+
+class MvlmError(RuntimeError):
+    def __init__(self, code: int, fn: str, msg: str):
+        super().__init__(f"{fn} failed with status {code}: {msg}")
+        self.code = code
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [("device_name", ctypes.c_char * 256), ("arch_name", ctypes.c_char * 64),
+                ("ordinal", c_int), ("compute_units", c_int), ("max_clock_mhz", c_int),
+                ("memory_clock_mhz", c_int), ("memory_bus_width_bits", c_int), ("wavefront_size", c_int),
+                ("global_mem_size", c_uint64), ("local_mem_size", c_uint64), ("l2_cache_size", c_uint64),
+                ("peak_hbm_gbs", c_double), ("peak_fp16_tflops", c_double)]
+
+
+_P = c_void_p
+_PP = POINTER(c_void_p)
+_SIGNATURES = {
+    "mvlm_last_error": (c_char_p, []),
+    "mvlm_abi_version": (c_int, []),
+    "mvlm_device_count": (c_int, [POINTER(c_int)]),
+    "mvlm_device_create": (c_int, [c_int, _PP]),
+    "mvlm_device_destroy": (c_int, [_P]),
+    "mvlm_device_get_info": (c_int, [_P, POINTER(DeviceInfo)]),
+    "mvlm_device_synchronize": (c_int, [_P]),
+    "mvlm_buffer_alloc": (c_int, [_P, c_size_t, _PP]),
+    "mvlm_buffer_view": (c_int, [_P, c_size_t, c_size_t, _PP]),
+    "mvlm_buffer_free": (c_int, [_P]),
+    "mvlm_buffer_size": (c_size_t, [_P]),
+    "mvlm_buffer_upload": (c_int, [_P, c_size_t, c_void_p, c_size_t]),
+    "mvlm_buffer_download": (c_int, [_P, c_size_t, c_void_p, c_size_t]),
+    "mvlm_buffer_fill_zero": (c_int, [_P]),
+    "mvlm_pool_init": (c_int, [_P, c_size_t, _PP]),
+    "mvlm_pool_current": (c_void_p, [_P]),
+    "mvlm_pool_next": (c_void_p, [_P]),
+    "mvlm_pool_swap": (c_int, [_P]),
+    "mvlm_pool_destroy": (c_int, [_P]),
+    "mvlm_weight_pack": (c_int, [_P, c_void_p, c_int, c_int, c_int, c_int, _PP]),
+    "mvlm_weight_pack_device": (c_int, [_P, _P, c_int, c_int, c_int, c_int, _PP]),
+    "mvlm_weight_free": (c_int, [_P]),
+    "mvlm_weight_dtype": (c_int, [_P]),
+    "mvlm_weight_shape": (c_int, [_P, POINTER(c_int), POINTER(c_int)]),
+    "mvlm_weight_bytes": (c_size_t, [_P]),
+    "mvlm_weight_dequant": (c_int, [_P, _P, _P, _PP]),
+    "mvlm_gemm_naive": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _PP]),
+    "mvlm_gemm_tiled": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _PP]),
+    "mvlm_gemm_packed": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, c_int, c_int, _PP]),
+    "mvlm_gemv": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, c_int, _PP]),
+    "mvlm_gemv_q8_0": (c_int, [_P, _P, _P, _P, c_int, c_int, _PP]),
+    "mvlm_gemv_q4_0": (c_int, [_P, _P, _P, _P, c_int, c_int, _PP]),
+    "mvlm_gemm_q8_0": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _PP]),
+    "mvlm_gemm_q4_0": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _PP]),
+    "mvlm_gemm_batched": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int,
+                                  c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, _PP]),
+    "mvlm_fill_normal": (c_int, [_P, _P, c_int, c_size_t, c_uint64, c_double]),
+    "mvlm_weight_random": (c_int, [_P, c_int, c_int, c_int, c_uint64, c_double, _PP]),
+    "mvlm_event_wait": (c_int, [_P]),
+    "mvlm_event_elapsed_ms": (c_int, [_P, POINTER(c_float)]),
+    "mvlm_event_release": (c_int, [_P]),
+    "mvlm_plan_create": (c_int, [_P, _PP]),
+    "mvlm_plan_destroy": (c_int, [_P]),
+    "mvlm_plan_size": (c_int, [_P]),
+    "mvlm_plan_add_gemv": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int]),
+    "mvlm_plan_add_gemm_packed": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int]),
+    "mvlm_plan_add_gemm_batched": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int,
+                                           c_int64, c_int64, c_int64, c_int64, c_int64, c_int64]),
+    "mvlm_plan_use_graph": (c_int, [_P, c_int]),
+    "mvlm_plan_run": (c_int, [_P, c_int, _PP]),
+    "mvlm_plan_profile": (c_int, [_P, POINTER(c_float), c_int]),
+    "mvlm_marker_record": (c_int, [_P, _PP]),
+    "mvlm_marker_elapsed_ms": (c_int, [_P, _P, POINTER(c_float)]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load the HIP library; raise if it is missing (no fallback path exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is not built; run `python -m mvlm_amd.build` "
+                              "(or __graft_entry__.build()) first")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return (lib().mvlm_last_error() or b"").decode()
+
+
+def check(status: int, fn: str) -> None:
+    if status != OK:
+        raise MvlmError(status, fn, last_error())
+
+
+def _call(name, *args):
+    check(getattr(lib(), name)(*args), name)
+
+
+def device_count() -> int:
+    n = c_int(0)
+    _call("mvlm_device_count", byref(n))
+    return n.value
+
+
+class Event:
+    def __init__(self, handle):
+        self.handle = handle
+
+    def elapsed_ms(self) -> float:
+        ms = c_float(0.0)
+        _call("mvlm_event_elapsed_ms", self.handle, byref(ms))
+        return ms.value
+
+    def wait(self) -> None:
+        _call("mvlm_event_wait", self.handle)
+
+    def release(self) -> None:
+        if self.handle:
+            _call("mvlm_event_release", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+
+class Buffer:
+    def __init__(self, dev: "Device", handle, nbytes: int, parent: "Buffer | None" = None):
+        self.dev, self.handle, self.nbytes, self.parent = dev, handle, nbytes, parent
+
+    def upload(self, arr: np.ndarray, offset: int = 0) -> "Buffer":
+        a = np.ascontiguousarray(arr)
+        _call("mvlm_buffer_upload", self.handle, offset, a.ctypes.data, a.nbytes)
+        return self
+
+    def download(self, dtype, count: int | None = None, offset: int = 0) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dtype.itemsize
+        out = np.empty(count, dtype)
+        _call("mvlm_buffer_download", self.handle, offset, out.ctypes.data, out.nbytes)
+        return out
+
+    def zero(self) -> "Buffer":
+        _call("mvlm_buffer_fill_zero", self.handle)
+        return self
+
+    def view(self, offset: int, nbytes: int) -> "Buffer":
+        h = c_void_p()
+        _call("mvlm_buffer_view", self.handle, offset, nbytes, byref(h))
+        return Buffer(self.dev, h, nbytes, parent=self)
+
+    def free(self) -> None:
+        if self.handle:
+            _call("mvlm_buffer_free", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Weight:
+    def __init__(self, dev: "Device", handle):
+        self.dev, self.handle = dev, handle
+
+    @property
+    def dtype(self) -> int:
+        return lib().mvlm_weight_dtype(self.handle)
+
+    @property
+    def shape(self):
+        n, k = c_int(), c_int()
+        _call("mvlm_weight_shape", self.handle, byref(n), byref(k))
+        return n.value, k.value
+
+    @property
+    def nbytes(self) -> int:
+        return lib().mvlm_weight_bytes(self.handle)
+
+    def dequant(self) -> np.ndarray:
+        n, k = self.shape
+        out = self.dev.alloc(n * k * 4)
+        _call("mvlm_weight_dequant", self.dev.handle, self.handle, out.handle, None)
+        self.dev.sync()
+        return out.download(np.float32).reshape(n, k)
+
+    def free(self) -> None:
+        if self.handle:
+            _call("mvlm_weight_free", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def _ev(want: bool):
+    return (c_void_p(), True) if want else (None, False)
+
+
+class Plan:
+    """A recorded launch sequence run from native code (eagerly or as a HIP graph).
+    Keeps references to the buffers and weights it names so they outlive it."""
+
+    def __init__(self, dev: "Device"):
+        self.dev = dev
+        h = c_void_p()
+        _call("mvlm_plan_create", dev.handle, byref(h))
+        self.handle = h
+        self._keep = []
+
+    def __len__(self):
+        return lib().mvlm_plan_size(self.handle)
+
+    def add_gemv(self, x, x_dtype, W, y, y_dtype, M=1):
+        _call("mvlm_plan_add_gemv", self.handle, x.handle, x_dtype, W.handle, y.handle, y_dtype, M)
+        self._keep += [x, W, y]
+        return self
+
+    def add_gemm_packed(self, A, a_dtype, W, C, c_dtype, M):
+        _call("mvlm_plan_add_gemm_packed", self.handle, A.handle, a_dtype, W.handle, C.handle, c_dtype, M)
+        self._keep += [A, W, C]
+        return self
+
+    def add_gemm_batched(self, A, B, C, batch, M, N, K, lda, ldb, ldc, sA, sB, sC):
+        _call("mvlm_plan_add_gemm_batched", self.handle, A.handle, B.handle, C.handle, batch, M, N, K,
+              lda, ldb, ldc, sA, sB, sC)
+        self._keep += [A, B, C]
+        return self
+
+    def use_graph(self, enable=True):
+        _call("mvlm_plan_use_graph", self.handle, 1 if enable else 0)
+        return self
+
+    def run(self, repeats=1, event=False):
+        ev, want = _ev(event)
+        _call("mvlm_plan_run", self.handle, repeats, byref(ev) if want else None)
+        return Event(ev) if want else None
+
+    def profile(self) -> np.ndarray:
+        n = len(self)
+        out = (c_float * n)()
+        _call("mvlm_plan_profile", self.handle, out, n)
+        return np.frombuffer(out, np.float32).copy()
+
+    def destroy(self):
+        if self.handle:
+            _call("mvlm_plan_destroy", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+class Device:
+    """One HIP device with its in-order stream (the DeviceInfo of the reference)."""
+
+    def __init__(self, ordinal: int = 0):
+        h = c_void_p()
+        _call("mvlm_device_create", ordinal, byref(h))
+        self.handle = h
+
+    def info(self) -> DeviceInfo:
+        inf = DeviceInfo()
+        _call("mvlm_device_get_info", self.handle, byref(inf))
+        return inf
+
+    def sync(self) -> None:
+        _call("mvlm_device_synchronize", self.handle)
+
+    def close(self) -> None:
+        if self.handle:
+            _call("mvlm_device_destroy", self.handle)
+            self.handle = None
+
+    # -- memory -------------------------------------------------------------
+    def alloc(self, nbytes: int) -> Buffer:
+        h = c_void_p()
+        _call("mvlm_buffer_alloc", self.handle, nbytes, byref(h))
+        return Buffer(self, h, nbytes)
+
+    def upload(self, arr: np.ndarray, pad_bytes: int = 0) -> Buffer:
+        a = np.ascontiguousarray(arr)
+        b = self.alloc(max(a.nbytes + pad_bytes, 1))
+        if a.nbytes:
+            b.upload(a)
+        return b
+
+    def pack(self, src: np.ndarray, dtype: int, N: int, K: int, layout: int = LAYOUT_NK) -> Weight:
+        a = np.ascontiguousarray(src)
+        h = c_void_p()
+        _call("mvlm_weight_pack", self.handle, a.ctypes.data, dtype, layout, N, K, byref(h))
+        return Weight(self, h)
+
+    def pack_device(self, src: Buffer, dtype: int, N: int, K: int, layout: int = LAYOUT_NK) -> Weight:
+        h = c_void_p()
+        _call("mvlm_weight_pack_device", self.handle, src.handle, dtype, layout, N, K, byref(h))
+        return Weight(self, h)
+
+    def random_weight(self, dtype: int, N: int, K: int, seed: int, wstd: float = 0.02) -> Weight:
+        h = c_void_p()
+        _call("mvlm_weight_random", self.handle, dtype, N, K, seed, wstd, byref(h))
+        return Weight(self, h)
+
+    def fill_normal(self, buf: Buffer, dtype: int, count: int, seed: int, std: float = 1.0) -> Buffer:
+        _call("mvlm_fill_normal", self.handle, buf.handle, dtype, count, seed, std)
+        return buf
+
+    def marker(self) -> Event:
+        h = c_void_p()
+        _call("mvlm_marker_record", self.handle, byref(h))
+        return Event(h)
+
+    # -- launches (event=True returns an Event timing the launch) -------------
+    def _launch(self, name, args, event):
+        ev, want = _ev(event)
+        _call(name, self.handle, *args, byref(ev) if want else None)
+        return Event(ev) if want else None
+
+    def gemm_naive(self, A, B, C, M, N, K, event=False):
+        return self._launch("mvlm_gemm_naive", (A.handle, B.handle, C.handle, M, N, K), event)
+
+    def gemm_tiled(self, A, B, C, M, N, K, event=False):
+        return self._launch("mvlm_gemm_tiled", (A.handle, B.handle, C.handle, M, N, K), event)
+
+    def gemm_packed(self, A, a_dtype, W, C, c_dtype, M, N, K, event=False):
+        return self._launch("mvlm_gemm_packed", (A.handle, a_dtype, W.handle, C.handle, c_dtype, M, N, K), event)
+
+    def gemv(self, x, x_dtype, W, y, y_dtype, N, K, event=False):
+        return self._launch("mvlm_gemv", (x.handle, x_dtype, W.handle, y.handle, y_dtype, N, K), event)
+
+    def gemv_q8_0(self, x, W, y, N, K, event=False):
+        return self._launch("mvlm_gemv_q8_0", (x.handle, W.handle, y.handle, N, K), event)
+
+    def gemv_q4_0(self, x, W, y, N, K, event=False):
+        return self._launch("mvlm_gemv_q4_0", (x.handle, W.handle, y.handle, N, K), event)
+
+    def gemm_q8_0(self, X, W, Y, M, N, K, event=False):
+        return self._launch("mvlm_gemm_q8_0", (X.handle, W.handle, Y.handle, M, N, K), event)
+
+    def gemm_q4_0(self, X, W, Y, M, N, K, event=False):
+        return self._launch("mvlm_gemm_q4_0", (X.handle, W.handle, Y.handle, M, N, K), event)
+
+    def gemm_batched(self, A, B, C, batch, M, N, K, lda, ldb, ldc, sA, sB, sC, event=False):
+        return self._launch("mvlm_gemm_batched", (A.handle, B.handle, C.handle, batch, M, N, K,
+                                                  lda, ldb, ldc, sA, sB, sC), event)
+
+    def gemm_quant(self, X, W, Y, M, N, K, event=False):
+        """Dispatch by the weight's dtype (Q8_0 or Q4_0)."""
+        fn = self.gemm_q8_0 if W.dtype == Q8_0 else self.gemm_q4_0
+        return fn(X, W, Y, M, N, K, event=event)

@@ -1,0 +1,368 @@
+"""GPU parity: every entry point of the C ABI against the CPU oracle.
+
+Bars (stated per test):
+  * gemm_naive / gemm_tiled: bit-exact fp16 (same per-output fma order as the
+    reference's gemm.cl:26-136 and its restatement).
+  * dequantized Q8_0 / Q4_0 weights: bit-exact against the GGUF definition.
+  * fp32 inputs (fp32 GEMV, dequantizing GEMV/GEMM): |y - r| <= 1e-5 * S,
+    S = sum_k |x_k w_k| (fp64), r the oracle's fp32 result.
+  * fp16 / bf16 inputs with fp32 accumulation: |y - r| <= 1e-3 * S, plus half
+    a unit in the last place of the output type when the output is 16-bit.
+"""
+import numpy as np
+import pytest
+
+import mvlm_amd as m
+from conftest import within
+
+pytestmark = pytest.mark.gpu
+
+F32, F16, BF16, Q8, Q4 = m.F32, m.F16, m.BF16, m.Q8_0, m.Q4_0
+
+
+def half_ulp(v, dtype):
+    v = np.abs(np.asarray(v, np.float64))
+    if dtype == F32:
+        return np.zeros_like(v)
+    if dtype == F16:
+        return 0.5 * np.spacing(v.astype(np.float16)).astype(np.float64) + 2.0 ** -25
+    # bf16: 8 significant bits
+    e = np.floor(np.log2(np.maximum(v, 1e-38)))
+    return 0.5 * 2.0 ** (e - 7)
+
+
+def widen(orc, arr, dtype):
+    if dtype == F32:
+        return np.asarray(arr, np.float32).astype(np.float64)
+    return (orc.f16_to_f32(arr) if dtype == F16 else orc.bf16_to_f32(arr)).astype(np.float64)
+
+
+def out_to_f64(orc, raw, dtype):
+    return widen(orc, raw, dtype)
+
+
+def gen(orc, dtype, n, seed, std=1.0):
+    if dtype == F32:
+        return orc.normal_f32(n, seed, std)
+    return orc.normal_f16(n, seed, std) if dtype == F16 else orc.normal_bf16(n, seed, std)
+
+
+def np_dtype(dtype):
+    return np.float32 if dtype == F32 else np.uint16
+
+
+# ---------------------------------------------------------------------------
+# reference-arithmetic GEMMs: bit-exact
+# ---------------------------------------------------------------------------
+
+REF_SHAPES = [(1, 1, 1), (1, 8192, 2048), (3, 5, 7), (17, 33, 9), (64, 64, 64), (65, 130, 100),
+              (32, 2048, 2048), (129, 70, 257)]
+
+
+@pytest.mark.parametrize("M,N,K", REF_SHAPES)
+def test_gemm_naive_and_tiled_bit_exact(dev, orc, M, N, K):
+    A = orc.normal_f16(M * K, 101)
+    B = orc.normal_f16(K * N, 102, 0.02)
+    ref16 = (orc.gemm_naive(A, B, M, N, K)[0] if M * N * K <= 2e6 else
+             orc.f32_to_f16(orc.gemm_nk("f16", A, B.reshape(K, N).T.copy(), M, N, K)))
+    dA, dB = dev.upload(A), dev.upload(B)
+    for fn in (dev.gemm_naive, dev.gemm_tiled):
+        dC = dev.alloc(M * N * 2)
+        fn(dA, dB, dC, M, N, K)
+        got = dC.download(np.uint16)
+        assert np.array_equal(got, ref16.ravel()), (fn.__name__, int(np.sum(got != ref16.ravel())))
+
+
+def test_reference_gemms_on_exact_integer_fixtures(dev, orc):
+    from test_oracle import golden_gemm_cases
+    for M, N, K, A, B, C16, _ in golden_gemm_cases():
+        dA, dB = dev.upload(A), dev.upload(B)
+        for fn in (dev.gemm_naive, dev.gemm_tiled):
+            dC = dev.alloc(M * N * 2)
+            fn(dA, dB, dC, M, N, K)
+            assert np.array_equal(dC.download(np.uint16), C16.ravel())
+        # the same integers through the packed MFMA path and the GEMV are exact too
+        W = dev.pack(B, F16, N, K, layout=m.LAYOUT_KN)
+        if K % 8 == 0:
+            dC = dev.alloc(M * N * 4)
+            dev.gemm_packed(dA, F16, W, dC, F32, M, N, K)
+            assert np.array_equal(dC.download(np.float32), C16.view(np.float16).astype(np.float32).ravel())
+        if M == 1:
+            y = dev.alloc(N * 2)
+            dev.gemv(dA, F16, W, y, F16, N, K)
+            assert np.array_equal(y.download(np.uint16), C16.ravel())
+
+
+# ---------------------------------------------------------------------------
+# dense GEMV
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("N,K", [(8192, 2048), (1, 1), (7, 3), (130, 1000), (2048, 8192), (51200, 2048)])
+def test_gemv_fp32(dev, orc, N, K):
+    """fp32 x, W, y (the fp32 GEMV of benchmarks/gemm_bench.cpp's llm_ffn shape): 1e-5 * S."""
+    x = orc.normal_f32(K, 111)
+    W = orc.normal_f32(N * K, 112, 0.02)
+    ref = orc.gemm_nk("f32", x, W, 1, N, K)[0]
+    _, S = orc.gemm_f64(x.astype(np.float64)[None], W.astype(np.float64).reshape(N, K), 1, N, K)
+    dW = dev.pack(W, F32, N, K)
+    dx, dy = dev.upload(x), dev.alloc(N * 4)
+    dev.gemv(dx, F32, dW, dy, F32, N, K)
+    ok, worst = within(dy.download(np.float32), ref, S[0], 1e-5)
+    assert ok, worst
+
+
+@pytest.mark.parametrize("wd,xd,yd", [(F16, F16, F16), (F16, F32, F32), (BF16, BF16, F32), (BF16, F32, BF16),
+                                      (F32, F16, F32)])
+@pytest.mark.parametrize("N,K", [(2048, 2048), (70, 300), (5, 8)])
+def test_gemv_dtypes(dev, orc, wd, xd, yd, N, K):
+    x = gen(orc, xd, K, 121)
+    Wt = gen(orc, wd, N * K, 122, 0.02)
+    xf, Wf = widen(orc, x, xd), widen(orc, Wt, wd).reshape(N, K)
+    ref, S = orc.gemm_f64(xf[None], Wf, 1, N, K)
+    dW = dev.pack(Wt, wd, N, K)
+    dx, dy = dev.upload(x), dev.alloc(N * 4)
+    dev.gemv(dx, xd, dW, dy, yd, N, K)
+    got = out_to_f64(orc, dy.download(np_dtype(yd), N), yd)
+    rtol = 1e-5 if (xd == F32 and wd == F32) else 1e-3
+    ok, worst = within(got, ref[0], S[0], rtol, half_ulp(ref[0], yd))
+    assert ok, worst
+
+
+@pytest.mark.parametrize("N,K", [(8192, 2048), (2048, 2048), (6, 300)])
+def test_gemv_reference_mode_matches_restated_gemv(dev, orc, N, K):
+    """fp16 x, fp16 W given as [K,N] like create_weight_image, fp16 y: the reference
+    gemv (gemm.cl:219-270) restated, compared within 1e-3 * S plus half an fp16 ulp."""
+    x = orc.normal_f16(K, 131)
+    B = orc.normal_f16(K * N, 132, 0.02)
+    ref16, ref32 = orc.gemv(x, B, N, K)
+    _, S = orc.gemm_f64(orc.f16_to_f32(x).astype(np.float64)[None],
+                        orc.f16_to_f32(B).astype(np.float64).reshape(K, N).T.copy(), 1, N, K)
+    W = dev.pack(B, F16, N, K, layout=m.LAYOUT_KN)
+    dx, dy = dev.upload(x), dev.alloc(N * 2)
+    dev.gemv(dx, F16, W, dy, F16, N, K)
+    got = orc.f16_to_f32(dy.download(np.uint16)).astype(np.float64)
+    ok, worst = within(got, ref32, S[0], 1e-3, half_ulp(ref32, F16))
+    assert ok, worst
+    # the great majority of outputs round to the very same fp16 as the reference
+    assert np.mean(dy.download(np.uint16) == ref16) > 0.95
+
+
+# ---------------------------------------------------------------------------
+# quantized weights
+# ---------------------------------------------------------------------------
+
+def make_quant(orc, qt, N, K, seed):
+    nb = N * K // 32
+    return orc.q8_0_blocks(nb, seed) if qt == Q8 else orc.q4_0_blocks(nb, seed)
+
+
+@pytest.mark.parametrize("qt", [Q8, Q4])
+@pytest.mark.parametrize("N,K", [(6144, 2048), (3, 32), (50, 96)])
+def test_dequant_bit_exact(dev, orc, qt, N, K):
+    blocks = make_quant(orc, qt, N, K, 141)
+    ref = (orc.dequant_q8_0 if qt == Q8 else orc.dequant_q4_0)(blocks).reshape(N, K)
+    W = dev.pack(blocks, qt, N, K)
+    got = W.dequant()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_known_answer_blocks(dev):
+    import json, os
+    path = os.path.join(os.path.dirname(__file__), "golden", "blocks_known_answer.json")
+    for case in json.load(open(path))["cases"]:
+        raw = np.frombuffer(bytes.fromhex(case["bytes"]), np.uint8).copy()
+        W = dev.pack(raw, Q8 if case["type"] == "q8_0" else Q4, 1, 32)
+        assert np.array_equal(W.dequant().ravel().view(np.uint32), np.array(case["bits"], np.uint32)), case["name"]
+
+
+QSHAPES = [(6144, 2048), (2048, 8192), (1, 32), (37, 96), (8192, 2048)]
+
+
+@pytest.mark.parametrize("qt", [Q8, Q4])
+@pytest.mark.parametrize("N,K", QSHAPES)
+def test_quant_gemv(dev, orc, qt, N, K):
+    x = orc.normal_f32(K, 151)
+    blocks = make_quant(orc, qt, N, K, 152)
+    kind = "q8_0" if qt == Q8 else "q4_0"
+    ref = orc.gemm_nk(kind, x, blocks, 1, N, K)[0]
+    deq = (orc.dequant_q8_0 if qt == Q8 else orc.dequant_q4_0)(blocks).astype(np.float64).reshape(N, K)
+    _, S = orc.gemm_f64(x.astype(np.float64)[None], deq, 1, N, K)
+    W = dev.pack(blocks, qt, N, K)
+    dx, dy = dev.upload(x), dev.alloc(N * 4)
+    (dev.gemv_q8_0 if qt == Q8 else dev.gemv_q4_0)(dx, W, dy, N, K)
+    ok, worst = within(dy.download(np.float32), ref, S[0], 1e-5)
+    assert ok, worst
+    # the generic gemv entry (dispatch_gemv) serves quantized weights too
+    dy2 = dev.alloc(N * 4)
+    dev.gemv(dx, F32, W, dy2, F32, N, K)
+    assert np.array_equal(dy2.download(np.float32), dy.download(np.float32))
+
+
+@pytest.mark.parametrize("qt", [Q8, Q4])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 11, 16])
+def test_quant_skinny_gemm(dev, orc, qt, M):
+    N, K = 2048, 2048
+    X = orc.normal_f32(M * K, 161)
+    blocks = make_quant(orc, qt, N, K, 162)
+    kind = "q8_0" if qt == Q8 else "q4_0"
+    ref = orc.gemm_nk(kind, X, blocks, M, N, K)
+    deq = (orc.dequant_q8_0 if qt == Q8 else orc.dequant_q4_0)(blocks).astype(np.float64).reshape(N, K)
+    _, S = orc.gemm_f64(X.astype(np.float64).reshape(M, K), deq, M, N, K)
+    W = dev.pack(blocks, qt, N, K)
+    dX, dY = dev.upload(X), dev.alloc(M * N * 4)
+    dev.gemm_quant(dX, W, dY, M, N, K)
+    ok, worst = within(dY.download(np.float32).reshape(M, N), ref, S, 1e-5)
+    assert ok, worst
+
+
+def test_weight_random_matches_oracle_generator(dev, orc):
+    N, K, seed = 64, 256, 0x1234
+    for qt in (Q8, Q4):
+        W = dev.random_weight(qt, N, K, seed, 0.02)
+        blocks = make_quant(orc, qt, N, K, seed)
+        ref = (orc.dequant_q8_0 if qt == Q8 else orc.dequant_q4_0)(blocks).reshape(N, K)
+        got = W.dequant()
+        # codes are integer arithmetic (exact); scales pass through fp64 log/sin/cos,
+        # whose last bit may differ between libraries, so allow one fp16 ulp in d
+        same = got == ref
+        assert same.mean() > 0.99
+        assert np.allclose(got, ref, rtol=2 ** -10, atol=0)
+
+
+def test_fill_normal_matches_oracle_generator(dev, orc):
+    n = 10000
+    buf = dev.alloc(n * 4)
+    dev.fill_normal(buf, F32, n, 77, 1.0)
+    got = buf.download(np.float32)
+    ref = orc.normal_f32(n, 77)
+    assert np.allclose(got, ref, rtol=1e-6, atol=1e-7)
+
+
+# ---------------------------------------------------------------------------
+# packed MFMA GEMM and batched QK^T
+# ---------------------------------------------------------------------------
+
+def check_packed(dev, orc, M, N, K, ab, cd, layout=m.LAYOUT_NK, rows=None, seed=171):
+    A = gen(orc, ab, M * K, seed)
+    Wt = gen(orc, ab, N * K, seed + 1, 0.02)
+    src = Wt if layout == m.LAYOUT_NK else Wt.reshape(N, K).T.copy()
+    W = dev.pack(src, ab, N, K, layout=layout)
+    dA, dC = dev.upload(A), dev.alloc(M * N * 4)
+    dev.gemm_packed(dA, ab, W, dC, cd, M, N, K)
+    got = out_to_f64(orc, dC.download(np_dtype(cd), M * N), cd).reshape(M, N)
+    sel = np.arange(M) if rows is None else np.unique(np.linspace(0, M - 1, rows).astype(int))
+    Asel = A.reshape(M, K)[sel].copy()
+    ref = orc.gemm_nk("f16" if ab == F16 else "bf16", Asel, Wt, len(sel), N, K)
+    _, S = orc.gemm_f64(widen(orc, Asel, ab).reshape(len(sel), K), widen(orc, Wt, ab).reshape(N, K), len(sel), N, K)
+    ok, worst = within(got[sel], ref, S, 1e-3, half_ulp(ref, cd))
+    assert ok, worst
+    return worst
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 8), (5, 7, 16), (33, 65, 40), (129, 130, 200), (64, 128, 2048),
+                                   (200, 300, 8)])
+@pytest.mark.parametrize("ab,cd", [(F16, F32), (F16, F16), (BF16, F32), (BF16, BF16)])
+def test_gemm_packed_small(dev, orc, M, N, K, ab, cd):
+    check_packed(dev, orc, M, N, K, ab, cd)
+
+
+@pytest.mark.parametrize("M,N,K", [(768, 6144, 2048), (768, 8192, 2048), (768, 2048, 8192),
+                                   (729, 3456, 1152), (729, 1152, 1152), (729, 4304, 1152), (729, 1152, 4304)])
+def test_gemm_packed_model_shapes(dev, orc, M, N, K):
+    """The Phi-1.5 prefill and SigLIP linears; every output column, 24 rows spread over M."""
+    check_packed(dev, orc, M, N, K, F16, F32, rows=24)
+
+
+def test_gemm_packed_kn_layout_equals_nk(dev, orc):
+    check_packed(dev, orc, 50, 72, 96, F16, F32, layout=m.LAYOUT_KN)
+
+
+def test_gemm_batched_qk(dev, orc):
+    """16 heads of 729 x 72 . 72 x 729, Q and K head-interleaved [729, 16, 72] (attention.cl:44)."""
+    H, S, D = 16, 729, 72
+    Q = orc.normal_f16(S * H * D, 181)
+    Kt = orc.normal_f16(S * H * D, 182)
+    dQ, dK, dC = dev.upload(Q), dev.upload(Kt), dev.alloc(H * S * S * 4)
+    dev.gemm_batched(dQ, dK, dC, H, S, S, D, H * D, H * D, S, D, D, S * S)
+    got = dC.download(np.float32).reshape(H, S, S)
+    for h in (0, 7, 15):
+        q = Q.reshape(S, H, D)[:, h, :].copy()
+        k = Kt.reshape(S, H, D)[:, h, :].copy()
+        ref = orc.gemm_nk("f16", q, k, S, S, D)
+        _, Sc = orc.gemm_f64(orc.f16_to_f32(q).astype(np.float64), orc.f16_to_f32(k).astype(np.float64), S, S, D)
+        ok, worst = within(got[h], ref, Sc, 1e-3)
+        assert ok, (h, worst)
+
+
+# ---------------------------------------------------------------------------
+# buffers, pool, events, host-side errors with a live device
+# ---------------------------------------------------------------------------
+
+def test_buffers_views_and_pool(dev):
+    import ctypes
+    from mvlm_amd import native
+    b = dev.alloc(1024)
+    b.upload(np.arange(256, dtype=np.float32))
+    v = b.view(512, 256)
+    assert np.array_equal(v.download(np.float32), np.arange(128, 192, dtype=np.float32))
+    with pytest.raises(native.MvlmError) as e:
+        b.free()                       # a live view keeps the parent
+    assert e.value.code == native.ERR_INVALID_ARG
+    v.free()
+    b.zero()
+    dev.sync()
+    assert not b.download(np.float32).any()
+    L = native.lib()
+    pool = ctypes.c_void_p()
+    native.check(L.mvlm_pool_init(dev.handle, 4096, ctypes.byref(pool)), "pool_init")
+    cur, nxt = L.mvlm_pool_current(pool), L.mvlm_pool_next(pool)
+    assert cur and nxt and cur != nxt
+    native.check(L.mvlm_pool_swap(pool), "swap")
+    assert L.mvlm_pool_current(pool) == nxt and L.mvlm_pool_next(pool) == cur
+    assert L.mvlm_buffer_size(cur) == 4096
+    native.check(L.mvlm_pool_destroy(pool), "destroy")
+
+
+def test_errors_with_live_device(dev):
+    from mvlm_amd import native
+    A, B, C = dev.alloc(64), dev.alloc(64), dev.alloc(8)
+    with pytest.raises(native.MvlmError) as e:
+        dev.gemm_naive(A, B, C, 4, 4, 4)           # C needs 32 bytes
+    assert e.value.code == native.ERR_BUFFER_TOO_SMALL
+    with pytest.raises(native.MvlmError) as e:
+        dev.gemm_naive(A, B, C, 0, 4, 4)
+    assert e.value.code == native.ERR_INVALID_ARG
+    with pytest.raises(native.MvlmError) as e:
+        dev.pack(np.zeros(18 * 2, np.uint8), Q4, 2, 30)   # K not a multiple of 32
+    assert e.value.code == native.ERR_INVALID_ARG
+    W = dev.pack(np.zeros(34 * 2, np.uint8), Q8, 1, 64)
+    x, y = dev.alloc(64 * 4 * 17), dev.alloc(4 * 17)
+    with pytest.raises(native.MvlmError) as e:
+        dev.gemm_q8_0(x, W, y, 17, 1, 64)          # M above 16
+    assert e.value.code == native.ERR_INVALID_ARG
+    with pytest.raises(native.MvlmError) as e:
+        dev.gemv_q4_0(x, W, y, 1, 64)              # wrong weight type
+    assert e.value.code == native.ERR_INVALID_ARG
+    Wf = dev.pack(np.zeros(3 * 12, np.uint16), F16, 3, 12)
+    with pytest.raises(native.MvlmError) as e:
+        dev.gemm_packed(dev.alloc(12 * 2 * 2), F16, Wf, dev.alloc(64), F32, 2, 3, 12)   # K % 8
+    assert e.value.code == native.ERR_UNSUPPORTED
+
+
+def test_event_timing(dev, orc):
+    N, K = 8192, 2048
+    W = dev.random_weight(Q8, N, K, 5)
+    x, y = dev.alloc(K * 4), dev.alloc(N * 4)
+    dev.fill_normal(x, F32, K, 6)
+    ev = dev.gemv_q8_0(x, W, y, N, K, event=True)
+    ev.wait()
+    ms = ev.elapsed_ms()
+    assert 0.0 < ms < 100.0
+    m0 = dev.marker()
+    dev.gemv_q8_0(x, W, y, N, K)
+    m1 = dev.marker()
+    from mvlm_amd import native
+    import ctypes
+    t = ctypes.c_float()
+    native.check(native.lib().mvlm_marker_elapsed_ms(m0.handle, m1.handle, ctypes.byref(t)), "marker")
+    assert t.value > 0.0

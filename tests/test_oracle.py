@@ -1,0 +1,237 @@
+"""Pins the CPU oracle (oracle/oracle.c) before anything is checked against it.
+
+Each restated function meets at least one check that does not retype its
+formula: committed golden fixtures, numpy's independent float16 conversion,
+exact-integer cases where every summation order agrees bit for bit, closed
+forms (one-hot, identity), fp64 brute force, and cross-checks between the
+restatements of kernels that share an fma order in the reference
+(gemm_naive, gemm_tiled and gemm_image, src/kernels/gemm.cl:26-200).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from conftest import within
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def load_blocks():
+    with open(os.path.join(GOLDEN, "blocks_known_answer.json")) as f:
+        return json.load(f)
+
+
+# ---- number formats ----------------------------------------------------------
+
+def test_f16_rne_matches_numpy(orc):
+    rng = np.random.default_rng(7)
+    bits = rng.integers(0, 2 ** 32, 400_000, dtype=np.uint64).astype(np.uint32)
+    # add every boundary neighbourhood: ties, subnormal edge, overflow edge
+    edges = np.array([0x33000000, 0x33000001, 0x387FE000, 0x38800000, 0x477FEFFF, 0x477FF000,
+                      0x3F801000, 0x3F803000, 0x7F800000, 0x00000001], np.uint32)
+    bits = np.concatenate([bits, edges, edges | 0x80000000])
+    f = bits.view(np.float32)
+    mine = orc.f32_to_f16(f)
+    with np.errstate(over="ignore"):
+        ref = f.astype(np.float16).view(np.uint16)
+    finite = ~np.isnan(f)
+    assert np.array_equal(mine[finite], ref[finite])
+    assert np.all(np.isnan(orc.f16_to_f32(mine[~finite])))
+
+
+def test_f16_widen_all_patterns(orc):
+    allh = np.arange(65536, dtype=np.uint16)
+    mine = orc.f16_to_f32(allh)
+    ref = allh.view(np.float16).astype(np.float32)
+    same = (mine.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(mine) & np.isnan(ref))
+    assert same.all()
+
+
+def test_bf16_rne(orc):
+    # every bf16 value round-trips; the midpoint between two neighbours rounds to the even one
+    allb = np.arange(65536, dtype=np.uint16)
+    f = orc.bf16_to_f32(allb)
+    fin = ~np.isnan(f)
+    assert np.array_equal(orc.f32_to_bf16(f[fin]), allb[fin])
+    lo = np.arange(0x3F80, 0x3FA0, dtype=np.uint32)
+    mid = ((lo << 16) | 0x8000).view(np.float32)
+    expect = np.where(lo % 2 == 0, lo, lo + 1).astype(np.uint16)
+    assert np.array_equal(orc.f32_to_bf16(mid), expect)
+    above = ((lo << 16) | 0x8001).view(np.float32)
+    assert np.array_equal(orc.f32_to_bf16(above), (lo + 1).astype(np.uint16))
+
+
+# ---- GGUF blocks ---------------------------------------------------------------
+
+def test_block_sizes_match_reference_tests(orc):
+    """tests/test_gguf.cpp:16-34 of the reference: F32 4, F16 2, Q4_0 18, Q8_0 34; blocks of 32."""
+    g = load_blocks()
+    ids = {"F32": 0, "F16": 1, "Q4_0": 2, "Q8_0": 8}
+    for name, tid in ids.items():
+        assert orc.lib().orc_ggml_type_size(tid) == g["type_sizes"][name]
+        assert orc.lib().orc_ggml_block_size(tid) == g["block_sizes"][name]
+
+
+def test_dequant_known_answer_blocks(orc):
+    for case in load_blocks()["cases"]:
+        raw = np.frombuffer(bytes.fromhex(case["bytes"]), np.uint8).copy()
+        out = orc.dequant_q8_0(raw) if case["type"] == "q8_0" else orc.dequant_q4_0(raw)
+        assert np.array_equal(out.view(np.uint32), np.array(case["bits"], np.uint32)), case["name"]
+
+
+def test_dequant_matches_brute_force_definition(orc):
+    """Random blocks against the definition evaluated in fp64 with numpy's fp16 decoding."""
+    nb = 500
+    q8 = orc.q8_0_blocks(nb, 11)
+    q4 = orc.q4_0_blocks(nb, 12)
+    blk8 = q8.reshape(nb, 34)
+    d8 = blk8[:, :2].copy().view(np.float16).astype(np.float64)
+    qs8 = blk8[:, 2:].view(np.int8).astype(np.float64)
+    assert np.array_equal(orc.dequant_q8_0(q8), (qs8 * d8).astype(np.float32).ravel())
+    blk4 = q4.reshape(nb, 18)
+    d4 = blk4[:, :2].copy().view(np.float16).astype(np.float64)
+    qs4 = blk4[:, 2:].astype(np.int64)
+    codes = np.concatenate([qs4 & 15, qs4 >> 4], axis=1).astype(np.float64) - 8.0
+    assert np.array_equal(orc.dequant_q4_0(q4), (codes * d4).astype(np.float32).ravel())
+
+
+def test_generated_block_distributions(orc):
+    nb = 4000
+    q8 = orc.q8_0_blocks(nb, 21).reshape(nb, 34)
+    qs = q8[:, 2:].view(np.int8)
+    assert qs.min() == -127 and qs.max() == 127           # never -128
+    d = q8[:, :2].copy().view(np.float16).astype(np.float64)
+    assert np.all(d >= 0) and abs(np.mean(d * 127) - 0.02 * np.sqrt(2 / np.pi)) < 1e-3
+    q4 = orc.q4_0_blocks(nb, 22).reshape(nb, 18)
+    codes = np.concatenate([q4[:, 2:] & 15, q4[:, 2:] >> 4])
+    assert codes.min() == 0 and codes.max() == 15
+    d4 = q4[:, :2].copy().view(np.float16).astype(np.float64)
+    assert abs(np.mean(d4 * 8) - 0.02 * np.sqrt(2 / np.pi)) < 1e-3
+
+
+def test_normal_generator_moments_and_determinism(orc):
+    x = orc.normal_f32(200_000, orc.seed_for(1))
+    assert abs(x.mean()) < 0.01 and abs(x.std() - 1.0) < 0.01
+    assert np.array_equal(x, orc.normal_f32(200_000, orc.seed_for(1)))
+    assert not np.array_equal(x[:100], orc.normal_f32(100, orc.seed_for(2)))
+    # counter-based: a prefix equals the first elements of a longer fill
+    assert np.array_equal(orc.normal_f32(1001, 5)[:1000], orc.normal_f32(1000, 5))
+    # Box-Muller pairs: even/odd elements share a radius, r^2 = x_even^2 + x_odd^2 = -2 ln u1
+    u1 = np.array([orc.lib().orc_uniform_at(5, 2 * j) for j in range(50)])
+    xx = orc.normal_f32(100, 5).astype(np.float64)
+    assert np.allclose(xx[0::2] ** 2 + xx[1::2] ** 2, -2 * np.log(u1), rtol=1e-6)
+
+
+# ---- restatements of gemm.cl ------------------------------------------------------
+
+def golden_gemm_cases():
+    z = np.load(os.path.join(GOLDEN, "gemm_exact_int.npz"))
+    i = 0
+    while f"case{i}_shape" in z:
+        M, N, K = (int(v) for v in z[f"case{i}_shape"])
+        yield M, N, K, z[f"case{i}_A"], z[f"case{i}_B"], z[f"case{i}_C16"], z[f"case{i}_C32"]
+        i += 1
+
+
+def test_reference_kernels_on_exact_integer_fixtures(orc):
+    for M, N, K, A, B, C16, C32 in golden_gemm_cases():
+        for fn in (orc.gemm_naive, orc.gemm_tiled, orc.gemm_image):
+            c16, c32 = fn(A, B, M, N, K)
+            assert np.array_equal(c16, C16) and np.array_equal(c32, C32)
+        if M == 1:
+            y16, y32 = orc.gemv(A[0], B, N, K)
+            assert np.array_equal(y16, C16[0]) and np.array_equal(y32, C32[0])
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (5, 9, 17), (13, 37, 45), (16, 16, 64), (3, 70, 300)])
+def test_naive_tiled_image_share_fma_order(orc, M, N, K):
+    A = orc.normal_f16(M * K, 31)
+    B = orc.normal_f16(K * N, 32, 0.02)
+    n16, n32 = orc.gemm_naive(A, B, M, N, K)
+    for fn in (orc.gemm_tiled, orc.gemm_image):
+        c16, c32 = fn(A, B, M, N, K)
+        assert np.array_equal(c16, n16) and np.array_equal(c32.view(np.uint32), n32.view(np.uint32))
+
+
+def test_gemv_against_fp64_and_naive(orc):
+    N, K = 67, 1000
+    x = orc.normal_f16(K, 41)
+    B = orc.normal_f16(K * N, 42, 0.02)
+    y16, y32 = orc.gemv(x, B, N, K)
+    xf = orc.f16_to_f32(x).astype(np.float64)[None, :]
+    Bf = orc.f16_to_f32(B).astype(np.float64).reshape(K, N)
+    ref, scale = orc.gemm_f64(xf, Bf.T.copy(), 1, N, K)
+    ok, worst = within(y32, ref[0], scale[0], 1e-6)
+    assert ok, worst
+    # the stored fp16 is the RNE rounding of the fp32 accumulator
+    assert np.array_equal(y16, orc.f32_to_f16(y32))
+    # a different partition of the same sum (tree vs chain) differs only by rounding
+    _, n32 = orc.gemm_naive(x, B, 1, N, K)
+    assert within(y32, n32[0], scale[0], 1e-6)[0]
+
+
+def test_closed_forms(orc):
+    K, N = 96, 40
+    B = orc.normal_f16(K * N, 51, 0.5)
+    for k in (0, 17, 95):
+        x = np.zeros(K, np.uint16)
+        x[k] = 0x3C00  # 1.0
+        y16, y32 = orc.gemv(x, B, N, K)
+        assert np.array_equal(y16, B.reshape(K, N)[k])
+        c16, _ = orc.gemm_naive(x, B, 1, N, K)
+        assert np.array_equal(c16[0], B.reshape(K, N)[k])
+    eye = np.eye(K, dtype=np.float16).view(np.uint16)
+    A = orc.normal_f16(7 * K, 52)
+    c16, _ = orc.gemm_tiled(A, eye, 7, K, K)
+    assert np.array_equal(c16, A.reshape(7, K))
+
+
+# ---- the NT path -------------------------------------------------------------------
+
+@pytest.mark.parametrize("kind", ["f32", "f16", "bf16", "q8_0", "q4_0"])
+def test_nt_gemm_against_fp64(orc, kind):
+    M, N, K = 3, 45, 256
+    if kind == "f32":
+        X = orc.normal_f32(M * K, 61); W = orc.normal_f32(N * K, 62, 0.02)
+        Xf, Wf = X.astype(np.float64), W.astype(np.float64)
+    elif kind in ("f16", "bf16"):
+        gen, wid = (orc.normal_f16, orc.f16_to_f32) if kind == "f16" else (orc.normal_bf16, orc.bf16_to_f32)
+        X = gen(M * K, 61); W = gen(N * K, 62, 0.02)
+        Xf, Wf = wid(X).astype(np.float64), wid(W).astype(np.float64)
+    else:
+        X = orc.normal_f32(M * K, 61)
+        W = orc.q8_0_blocks(N * K // 32, 62) if kind == "q8_0" else orc.q4_0_blocks(N * K // 32, 62)
+        deq = orc.dequant_q8_0 if kind == "q8_0" else orc.dequant_q4_0
+        Xf, Wf = X.astype(np.float64), deq(W).astype(np.float64)
+    Y = orc.gemm_nk(kind, X, W, M, N, K)
+    ref, scale = orc.gemm_f64(Xf.reshape(M, K), Wf.reshape(N, K), M, N, K)
+    ok, worst = within(Y, ref, scale, 1e-6)
+    assert ok, worst
+    # the thread count does not change any bit
+    assert np.array_equal(Y, orc.gemm_nk(kind, X, W, M, N, K, nthreads=1))
+
+
+def test_nt_gemm_is_transposed_reference_gemm(orc):
+    """The NT restatement of an fp16 product equals gemm_naive's fp32 accumulator on W^T:
+    same operands, same ascending-k fma chain."""
+    M, N, K = 4, 24, 130
+    X = orc.normal_f16(M * K, 71)
+    W = orc.normal_f16(N * K, 72, 0.02)
+    WT = W.reshape(N, K).T.copy()
+    _, n32 = orc.gemm_naive(X, WT, M, N, K)
+    Y = orc.gemm_nk("f16", X, W, M, N, K)
+    assert np.array_equal(Y.view(np.uint32), n32.view(np.uint32))
+
+
+def test_batched_against_per_head_products(orc):
+    H, S, D = 3, 19, 24
+    Q = orc.normal_f16(S * H * D, 81)
+    Kt = orc.normal_f16(S * H * D, 82)
+    C = orc.gemm_batched_f16(Q, Kt, H, S, S, D, H * D, H * D, S, D, D, S * S, H * S * S)
+    for h in range(H):
+        q = Q.reshape(S, H, D)[:, h, :].copy()
+        k = Kt.reshape(S, H, D)[:, h, :].copy()
+        ref = orc.gemm_nk("f16", q, k, S, S, D)
+        assert np.array_equal(C.reshape(H, S, S)[h], ref)
