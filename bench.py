@@ -64,7 +64,8 @@ def timed_plan(dev, plan, steps, warmup):
 
 
 def profile_plan(plan, reps=5):
-    """Per-launch device time (median over eager runs with a marker after each launch)."""
+    """Per-launch kernel execution time: median over eager runs in which each launch
+    carries HIP start/stop events on its own dispatch packet."""
     runs = np.stack([plan.profile() for _ in range(reps)])
     return np.median(runs, axis=0)
 
@@ -73,15 +74,32 @@ def profile_plan(plan, reps=5):
 # workloads
 # ---------------------------------------------------------------------------
 
-def decode_step(dev, m, qt, M, steps, warmup, graph=True):
-    """One Phi-1.5 decode step over quantized weights, M rows of activations."""
+def decode_step(dev, m, qt, M, steps, warmup, graph=True, grouped=True):
+    """One Phi-1.5 decode step over quantized weights, M rows of activations.
+
+    Phi-1.5 blocks are parallel (attention and MLP read the same normalised
+    input), so per layer QKV and fc1 are independent of each other, and so are
+    dense (on the attention output) and fc2 (on the GELU output).  grouped=True
+    issues each independent pair as one grouped launch (2 launches per layer +
+    the LM head = 49); grouped=False issues the 97 GEMVs one launch each."""
     qdt = m.Q8_0 if qt == "q8_0" else m.Q4_0
     weights = [dev.random_weight(qdt, N, K, SEED ^ (0x100 + i), 0.02) for i, (_, N, K) in enumerate(PHI_STEP)]
-    xs = {K: dev.fill_normal(dev.alloc(M * K * 4), m.F32, M * K, SEED ^ K, 1.0) for K in (2048, 8192)}
-    ys = {N: dev.alloc(M * N * 4) for N in (2048, 6144, 8192, 51200)}
+    ln = dev.fill_normal(dev.alloc(M * 2048 * 4), m.F32, M * 2048, SEED ^ 0x11, 1.0)     # block input
+    attn = dev.fill_normal(dev.alloc(M * 2048 * 4), m.F32, M * 2048, SEED ^ 0x12, 1.0)   # attention out
+    gelu = dev.fill_normal(dev.alloc(M * 8192 * 4), m.F32, M * 8192, SEED ^ 0x13, 1.0)   # MLP hidden
+    x_of = {"qkv": ln, "fc1": ln, "dense": attn, "fc2": gelu, "lm_head": ln}
+    ys = {name: dev.alloc(M * N * 4) for name, N, _ in PHI_LAYER + [PHI_LM_HEAD]}
+    grouped = grouped and M == 1
     plan = m.Plan(dev)
-    for W, (_, N, K) in zip(weights, PHI_STEP):
-        plan.add_gemv(xs[K], m.F32, W, ys[N], m.F32, M)
+    if grouped:
+        for layer in range(24):
+            w = dict(zip(("qkv", "dense", "fc1", "fc2"), weights[4 * layer: 4 * layer + 4]))
+            plan.add_gemv_grouped([(x_of[n], m.F32, w[n], ys[n], m.F32) for n in ("qkv", "fc1")])
+            plan.add_gemv_grouped([(x_of[n], m.F32, w[n], ys[n], m.F32) for n in ("dense", "fc2")])
+        plan.add_gemv(ln, m.F32, weights[-1], ys["lm_head"], m.F32, M)
+    else:
+        for W, (name, N, K) in zip(weights, PHI_STEP):
+            plan.add_gemv(x_of[name], m.F32, W, ys[name], m.F32, M)
     per_op = profile_plan(plan)
     if graph:
         plan.use_graph(True)
@@ -89,13 +107,18 @@ def decode_step(dev, m, qt, M, steps, warmup, graph=True):
     op_bytes = np.array([gemv_bytes(qt, N, K, M) for _, N, K in PHI_STEP], np.float64)
     step_bytes = float(op_bytes.sum())
     kernel_ms = float(per_op.sum())
+    if grouped:
+        launch_names = ["qkv+fc1", "dense+fc2"] * 24 + ["lm_head"]
+    else:
+        launch_names = [name for name, _, _ in PHI_STEP]
     res = {
-        "workload": f"phi15_decode_{qt}_m{M}", "M": M, "gemvs": len(PHI_STEP),
+        "workload": f"phi15_decode_{qt}_m{M}" + ("" if grouped or M > 1 else "_ungrouped"), "M": M,
+        "gemvs": len(PHI_STEP), "launches": len(launch_names),
         "bytes_per_step": step_bytes, "ms_per_step": ms, "gbs": step_bytes / ms / 1e6,
         "kernel_ms_sum": kernel_ms, "kernel_gbs": step_bytes / kernel_ms / 1e6,
         "flops_per_step": float(sum(2.0 * M * N * K for _, N, K in PHI_STEP)),
-        "per_shape_us": {name: float(np.median(per_op[[i for i, s in enumerate(PHI_STEP) if s[0] == name]]) * 1e3)
-                         for name in ("qkv", "dense", "fc1", "fc2", "lm_head")},
+        "per_launch_us": {name: float(np.median(per_op[[i for i, s in enumerate(launch_names) if s == name]]) * 1e3)
+                          for name in dict.fromkeys(launch_names)},
     }
     res["frac"] = res["gbs"] / PEAK_HBM_GBS
     res["kernel_frac"] = res["kernel_gbs"] / PEAK_HBM_GBS
@@ -215,8 +238,9 @@ def main():
 
     extra = {}
     if not args.quick:
-        for qt, M in (("q4_0", 1), ("q4_0", 4), ("q4_0", 16), ("q8_0", 4)):
-            r = decode_step(dev, m, qt, M, max(10, args.steps // 2), 3)
+        for qt, M, grp in (("q8_0", 1, False), ("q4_0", 1, True), ("q4_0", 1, False), ("q4_0", 4, True),
+                           ("q4_0", 16, True), ("q8_0", 4, True)):
+            r = decode_step(dev, m, qt, M, max(10, args.steps // 2), 3, grouped=grp)
             extra[r["workload"]] = r
             log(f"[bench]   {r['workload']}: {r['ms_per_step'] * 1e3:.1f} us/step {r['gbs']:.0f} GB/s "
                 f"({100 * r['frac']:.1f}%)")
@@ -257,14 +281,18 @@ def main():
         "data": "synthetic (SplitMix64/Box-Muller seeded Q8_0 blocks: qs uniform [-127,127], "
                 "d=f16(|N(0,0.02)|/127); x ~ N(0,1) fp32)",
         "config": {"workload": "phi15_decode_q8_0", "model": "Phi-1.5 weight set (24 layers, d=2048, ffn 8192, "
-                   "vocab 51200)", "gemvs_per_step": 97, "M": 1, "weight_format": "GGUF Q8_0 (packed split)",
+                   "vocab 51200)", "gemvs_per_step": 97, "launches_per_step": head["launches"], "M": 1,
+                   "weight_format": "GGUF Q8_0 (packed split)",
                    "bytes_per_step": head["bytes_per_step"], "graph": not args.eager,
+                   "grouping": "per layer {QKV, fc1} and {dense, fc2} as one launch each (independent in "
+                               "Phi-1.5's parallel block); LM head alone",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(head["kernel_gbs"], 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(head["kernel_frac"], 4), "traffic": None,
-                     "kernel": "gemv_q8_0_kernel",
-                     "timing": "sum over the 97 launches of one eager step of the HIP-event interval "
-                               "ending at each launch (median of 5 steps)"},
+                     "kernel": "gemv_stream_kernel<Q8Fmt>",
+                     "timing": f"algorithmic bytes of one step / sum of the {head['launches']} kernel "
+                               "execution times, each from HIP start/stop events on the launch's own dispatch "
+                               "(hipExtLaunchKernelGGL) on the plan's stream, median of 5 eager steps"},
         "cpu_baseline": cpu,
         "extra": extra,
     }

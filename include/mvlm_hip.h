@@ -151,6 +151,23 @@ int mvlm_gemm_packed(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, const 
 int mvlm_gemv(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W,
               mvlm_buffer* y, int y_dtype, int N, int K, mvlm_event** ev);
 
+/* ---- grouped decode GEMV ----------------------------------------------------
+ * Up to MVLM_MAX_GROUP independent GEMVs (M = 1) in one launch, e.g. the
+ * projections of one Phi-1.5 block that do not depend on each other: QKV and
+ * fc1 read the same input, dense and fc2 read the attention and MLP branches.
+ * The reference issues them as separate dispatch_gemv calls
+ * (src/models/moondream2.cpp:374-508).  All weights share one dtype and all
+ * x one dtype; each entry has the arguments and checks of mvlm_gemv. */
+#define MVLM_MAX_GROUP 8
+typedef struct mvlm_gemv_desc {
+    const mvlm_buffer* x;
+    int x_dtype;
+    const mvlm_weight* W;
+    mvlm_buffer* y;
+    int y_dtype;
+} mvlm_gemv_desc;
+int mvlm_gemv_grouped(mvlm_device* dev, int count, const mvlm_gemv_desc* descs, mvlm_event** ev);
+
 /* ---- dequantizing GEMV / skinny GEMM (planned in README.md:57, PLAN.md:65) */
 /* y[N] = x[K] * W^T, W packed Q8_0, x and y fp32. */
 int mvlm_gemv_q8_0(mvlm_device* dev, const mvlm_buffer* x, const mvlm_weight* W,
@@ -203,6 +220,7 @@ int mvlm_plan_size(const mvlm_plan* plan);
  * (mvlm_gemv); Q8_0 / Q4_0 W takes 1 <= M <= 16 (mvlm_gemm_q8_0/q4_0). */
 int mvlm_plan_add_gemv(mvlm_plan* plan, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W,
                        mvlm_buffer* y, int y_dtype, int M);
+int mvlm_plan_add_gemv_grouped(mvlm_plan* plan, int count, const mvlm_gemv_desc* descs);
 int mvlm_plan_add_gemm_packed(mvlm_plan* plan, const mvlm_buffer* A, int a_dtype, const mvlm_weight* W,
                               mvlm_buffer* C, int c_dtype, int M);
 int mvlm_plan_add_gemm_batched(mvlm_plan* plan, const mvlm_buffer* A, const mvlm_buffer* B,
@@ -213,8 +231,9 @@ int mvlm_plan_add_gemm_batched(mvlm_plan* plan, const mvlm_buffer* A, const mvlm
 int mvlm_plan_use_graph(mvlm_plan* plan, int enable);
 /* Enqueue the plan `repeats` times; `ev` (optional) spans everything enqueued. */
 int mvlm_plan_run(mvlm_plan* plan, int repeats, mvlm_event** ev);
-/* One eager run with a marker between launches: op_ms[i] is the device time
- * from the end of launch i-1 (the start, for i == 0) to the end of launch i. */
+/* One eager run in which every launch carries start/stop events on its own
+ * dispatch: op_ms[i] is the execution time of launch i (the figure
+ * rocprofv3 --kernel-trace reports for that dispatch). */
 int mvlm_plan_profile(mvlm_plan* plan, float* op_ms, int capacity);
 
 /* ---- stream markers for host-side timing of a region ---------------------- */

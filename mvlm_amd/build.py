@@ -71,9 +71,26 @@ def build(jobs: int = 8, verbose: bool = True) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}{r.stderr}")
     os.replace(tmp, LIB)
+    build_engine_test()
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {ENGINE_TEST}")
     return LIB
+
+
+ENGINE_TEST = os.path.join(LIBDIR, "test_engine")
+
+
+def build_engine_test() -> str:
+    """The C++ test of the mgpu:: drop-in (tests/cpp/test_engine.cpp): plain C++
+    over the C ABI, linked against the library next to it."""
+    src = os.path.join(ROOT, "tests", "cpp", "test_engine.cpp")
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-Wall", f"-I{os.path.join(ROOT, 'include')}",
+           f"-I{ENGINE}", src, "-o", ENGINE_TEST + ".tmp", f"-L{LIBDIR}", "-lmvlm_hip", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"engine test build failed:\n{' '.join(cmd)}\n{r.stdout}{r.stderr}")
+    os.replace(ENGINE_TEST + ".tmp", ENGINE_TEST)
+    return ENGINE_TEST
 
 
 def exported_symbols(path: str = LIB):

@@ -2,8 +2,11 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <hip/hip_fp16.h>
 #include <hip/hip_bf16.h>
+
+#include <utility>
 
 #include <cstdarg>
 #include <cstdint>
@@ -97,6 +100,26 @@ struct LaunchScope {
     int finish(const char* kernel_name);
 };
 
+// Every op enqueues exactly one kernel through launch_kernel.  When a caller
+// sets kernel_timing (plan profiling), the launch carries start/stop events on
+// its own dispatch packet (hipExtLaunchKernelGGL), which time the kernel's
+// execution without adding marker packets between launches.
+struct KernelTiming {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+KernelTiming& kernel_timing();
+
+template <typename... KArgs, typename... Args>
+inline void launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t shmem, hipStream_t s,
+                          Args&&... args) {
+    KernelTiming& t = kernel_timing();
+    if (t.start)
+        hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, t.start, t.stop, 0, std::forward<Args>(args)...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, shmem, s, std::forward<Args>(args)...);
+}
+
 // Kernel launchers (defined in the .hip files).  They assume validated input.
 hipError_t launch_gemm_naive(hipStream_t s, const uint16_t* A, const uint16_t* B, uint16_t* C,
                              int M, int N, int K);
@@ -106,6 +129,13 @@ hipError_t launch_gemv_dense(hipStream_t s, const void* x, int x_dtype, const mv
                              void* y, int y_dtype, int N, int K);
 hipError_t launch_gemv_quant(hipStream_t s, const float* X, const mvlm_weight* W, float* Y,
                              int M, int N, int K);
+// M == 1 streaming GEMV for every weight format (rows of at most 16 KiB).
+bool stream_supported(const mvlm_weight* w);
+hipError_t launch_gemv_stream(hipStream_t s, const void* x, int x_dtype, const mvlm_weight* W, void* y,
+                              int y_dtype, int num_cus);
+hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const* xs, int x_dtype,
+                                    const mvlm_weight* const* ws, void* const* ys, const int* y_dtypes);
+inline int64_t weight_row_bytes(const mvlm_weight* w) { return is_dense(w->dtype) ? w->ld * (int64_t)dtype_size(w->dtype) : w->ld; }
 hipError_t launch_gemm_mfma(hipStream_t s, const void* A, int ab_dtype, const void* B, void* C,
                             int c_dtype, int batch, int M, int N, int K, int64_t lda, int64_t ldb,
                             int64_t ldc, int64_t strideA, int64_t strideB, int64_t strideC,

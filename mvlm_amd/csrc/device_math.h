@@ -48,6 +48,16 @@ __device__ __forceinline__ float to_f32(__hip_bfloat16 v) { return bf16_bits_to_
 __device__ __forceinline__ float q8_value(int8_t q, float d) { return (float)q * d; }
 __device__ __forceinline__ float q4_value(int code, float d) { return (float)(code - 8) * d; }
 
+// v & 0x0F0F0F0F: the four low nibbles of v, one per byte.  Written as a
+// single v_and_b32 the compiler cannot see through, so that the following
+// (float)((r >> 8e) & 0xFF) become one v_cvt_f32_ubyte<e> each instead of a
+// v_bfe_u32 + v_cvt_f32_ubyte0 pair.
+__device__ __forceinline__ uint32_t nibbles_to_bytes(uint32_t v) {
+    uint32_t r;
+    asm("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(v), "v"(0x0F0F0F0Fu));
+    return r;
+}
+
 // Stores of an fp32 result in the requested output type.
 __device__ __forceinline__ void store_out(void* y, int64_t i, float v, int dtype) {
     if (dtype == 0) ((float*)y)[i] = v;                       // MVLM_F32

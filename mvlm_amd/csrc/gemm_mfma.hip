@@ -143,9 +143,9 @@ static void launch_typed(hipStream_t s, TileCfg t, const uint16_t* A, const uint
                          int batch, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
                          int64_t sA, int64_t sB, int64_t sC) {
     dim3 grid((N + t.bn - 1) / t.bn, (M + t.bm - 1) / t.bm, batch);
-#define MVLM_LAUNCH(BMv, BNv)                                                                      \
-    gemm_mfma_kernel<BF16, BMv, BNv><<<grid, 256, 0, s>>>(A, B, C, c_dtype, M, N, K, lda, ldb, ldc, \
-                                                         sA, sB, sC)
+#define MVLM_LAUNCH(BMv, BNv)                                                                         \
+    launch_kernel(gemm_mfma_kernel<BF16, BMv, BNv>, grid, dim3(256), 0, s, A, B, C, c_dtype, M, N, K, lda, \
+                  ldb, ldc, sA, sB, sC)
     if (t.bm == 128 && t.bn == 128) MVLM_LAUNCH(128, 128);
     else if (t.bm == 128) MVLM_LAUNCH(128, 64);
     else if (t.bn == 128) MVLM_LAUNCH(64, 128);

@@ -30,7 +30,7 @@ __global__ __launch_bounds__(256) void gemm_naive_kernel(const uint16_t* __restr
 hipError_t launch_gemm_naive(hipStream_t s, const uint16_t* A, const uint16_t* B, uint16_t* C,
                              int M, int N, int K) {
     dim3 grid((N + 15) / 16, (M + 15) / 16);
-    gemm_naive_kernel<<<grid, 256, 0, s>>>(A, B, C, M, N, K);
+    launch_kernel(gemm_naive_kernel, grid, dim3(256), 0, s, A, B, C, M, N, K);
     return hipGetLastError();
 }
 
@@ -96,7 +96,7 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(const uint16_t* __restr
 hipError_t launch_gemm_tiled(hipStream_t s, const uint16_t* A, const uint16_t* B, uint16_t* C,
                              int M, int N, int K) {
     dim3 grid((N + TT - 1) / TT, (M + TT - 1) / TT);
-    gemm_tiled_kernel<<<grid, 256, 0, s>>>(A, B, C, M, N, K);
+    launch_kernel(gemm_tiled_kernel, grid, dim3(256), 0, s, A, B, C, M, N, K);
     return hipGetLastError();
 }
 

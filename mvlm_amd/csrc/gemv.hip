@@ -118,9 +118,9 @@ static hipError_t launch_dense_xw(hipStream_t s, const void* x, const mvlm_weigh
     const XT* xp = (const XT*)x;
     const WT* wp = (const WT*)W->data;
     switch (R) {
-        case 4: gemv_dense_kernel<XT, WT, 4><<<grid, 256, 0, s>>>(xp, wp, W->ld, y, y_dtype, N, K); break;
-        case 2: gemv_dense_kernel<XT, WT, 2><<<grid, 256, 0, s>>>(xp, wp, W->ld, y, y_dtype, N, K); break;
-        default: gemv_dense_kernel<XT, WT, 1><<<grid, 256, 0, s>>>(xp, wp, W->ld, y, y_dtype, N, K); break;
+        case 4: launch_kernel(gemv_dense_kernel<XT, WT, 4>, dim3(grid), dim3(256), 0, s, xp, wp, W->ld, y, y_dtype, N, K); break;
+        case 2: launch_kernel(gemv_dense_kernel<XT, WT, 2>, dim3(grid), dim3(256), 0, s, xp, wp, W->ld, y, y_dtype, N, K); break;
+        default: launch_kernel(gemv_dense_kernel<XT, WT, 1>, dim3(grid), dim3(256), 0, s, xp, wp, W->ld, y, y_dtype, N, K); break;
     }
     return hipGetLastError();
 }

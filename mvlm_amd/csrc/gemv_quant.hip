@@ -115,8 +115,8 @@ __global__ __launch_bounds__(256) void gemv_q4_0_kernel(const float* __restrict_
         for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                uint32_t lo = q[r][i] & 0x0F0F0F0Fu;
-                uint32_t hi = (q[r][i] >> 4) & 0x0F0F0F0Fu;
+                const uint32_t lo = nibbles_to_bytes(q[r][i]);
+                const uint32_t hi = nibbles_to_bytes(q[r][i] >> 4);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     w[r][4 * i + e] = (float)((lo >> (8 * e)) & 0xFFu);
@@ -160,9 +160,11 @@ template <int R, int MT>
 static void launch_q(hipStream_t s, const float* X, const mvlm_weight* W, float* Y, int M, int N, int K) {
     unsigned grid = (unsigned)((N + 4 * R - 1) / (4 * R));
     if (W->dtype == MVLM_Q8_0)
-        gemv_q8_0_kernel<R, MT><<<grid, 256, 0, s>>>(X, (const int8_t*)W->data, (const uint16_t*)W->scales, Y, M, N, K);
+        launch_kernel(gemv_q8_0_kernel<R, MT>, dim3(grid), dim3(256), 0, s, X, (const int8_t*)W->data,
+                      (const uint16_t*)W->scales, Y, M, N, K);
     else
-        gemv_q4_0_kernel<R, MT><<<grid, 256, 0, s>>>(X, (const uint8_t*)W->data, (const uint16_t*)W->scales, Y, M, N, K);
+        launch_kernel(gemv_q4_0_kernel<R, MT>, dim3(grid), dim3(256), 0, s, X, (const uint8_t*)W->data,
+                      (const uint16_t*)W->scales, Y, M, N, K);
 }
 
 hipError_t launch_gemv_quant(hipStream_t s, const float* X, const mvlm_weight* W, float* Y, int M, int N, int K) {

@@ -15,7 +15,7 @@ using namespace mvlm;
 
 namespace {
 
-enum OpKind { OP_GEMM_NAIVE, OP_GEMM_TILED, OP_GEMM_MFMA, OP_GEMV_DENSE, OP_GEMV_QUANT };
+enum OpKind { OP_GEMM_NAIVE, OP_GEMM_TILED, OP_GEMM_MFMA, OP_GEMV_DENSE, OP_GEMV_QUANT, OP_GEMV_GROUP };
 
 struct Op {
     OpKind kind;
@@ -27,6 +27,12 @@ struct Op {
     int batch = 1, M = 0, N = 0, K = 0;
     int64_t lda = 0, ldb = 0, ldc = 0, sA = 0, sB = 0, sC = 0;
     int num_cus = 256;
+    // grouped GEMV
+    int gcount = 0;
+    const void* gx[MVLM_MAX_GROUP] = {};
+    const mvlm_weight* gw[MVLM_MAX_GROUP] = {};
+    void* gy[MVLM_MAX_GROUP] = {};
+    int gyd[MVLM_MAX_GROUP] = {};
 };
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -116,6 +122,7 @@ int make_gemv(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, const mvlm_we
     op->a = x->ptr; op->c = y->ptr; op->w = W;
     op->M = M; op->N = N; op->K = K;
     op->a_dtype = x_dtype; op->c_dtype = y_dtype;
+    op->num_cus = dev->prop.multiProcessorCount;
     if (is_quant(W->dtype)) {
         REQUIRE(M >= 1 && M <= 16, "%s: M=%d outside [1, 16]", fn, M);
         REQUIRE(x_dtype == MVLM_F32 && y_dtype == MVLM_F32, "%s: quantized weights take fp32 x and y", fn);
@@ -132,8 +139,38 @@ int make_gemv(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, const mvlm_we
     return MVLM_OK;
 }
 
+int make_gemv_group(mvlm_device* dev, int count, const mvlm_gemv_desc* descs, const char* fn, Op* op) {
+    REQUIRE(dev && descs, "%s: null argument", fn);
+    REQUIRE(count >= 1 && count <= MVLM_MAX_GROUP, "%s: count=%d outside [1, %d]", fn, count, MVLM_MAX_GROUP);
+    for (int i = 0; i < count; ++i) {
+        const mvlm_gemv_desc& d = descs[i];
+        REQUIRE(d.W, "%s: entry %d has no weight", fn, i);
+        Op one{};
+        int st = make_gemv(dev, d.x, d.x_dtype, d.W, d.y, d.y_dtype, 1, d.W->N, d.W->K, -1, fn, &one);
+        if (st != MVLM_OK) return st;
+        REQUIRE(d.W->dtype == descs[0].W->dtype, "%s: entry %d weight dtype %d differs from entry 0 (%d)", fn, i,
+                d.W->dtype, descs[0].W->dtype);
+        REQUIRE(d.x_dtype == descs[0].x_dtype, "%s: entry %d x dtype differs from entry 0", fn, i);
+        if (!stream_supported(d.W))
+            return set_error(MVLM_ERR_UNSUPPORTED, "%s: entry %d: rows of %lld bytes (K=%d) are outside the grouped "
+                             "kernel's range (<= 16 KiB, K a multiple of the 16-byte vector)", fn, i,
+                             (long long)weight_row_bytes(d.W), d.W->K);
+        op->gx[i] = d.x->ptr;
+        op->gw[i] = d.W;
+        op->gy[i] = d.y->ptr;
+        op->gyd[i] = d.y_dtype;
+    }
+    op->kind = OP_GEMV_GROUP;
+    op->gcount = count;
+    op->a_dtype = descs[0].x_dtype;
+    op->num_cus = dev->prop.multiProcessorCount;
+    return MVLM_OK;
+}
+
 hipError_t enqueue_op(hipStream_t s, const Op& op) {
     switch (op.kind) {
+        case OP_GEMV_GROUP:
+            return launch_gemv_stream_group(s, op.gcount, op.gx, op.a_dtype, op.gw, op.gy, op.gyd);
         case OP_GEMM_NAIVE:
             return launch_gemm_naive(s, (const uint16_t*)op.a, (const uint16_t*)op.b, (uint16_t*)op.c, op.M, op.N, op.K);
         case OP_GEMM_TILED:
@@ -142,8 +179,12 @@ hipError_t enqueue_op(hipStream_t s, const Op& op) {
             return launch_gemm_mfma(s, op.a, op.a_dtype, op.b, op.c, op.c_dtype, op.batch, op.M, op.N, op.K,
                                     op.lda, op.ldb, op.ldc, op.sA, op.sB, op.sC, op.num_cus);
         case OP_GEMV_DENSE:
+            if (stream_supported(op.w))
+                return launch_gemv_stream(s, op.a, op.a_dtype, op.w, op.c, op.c_dtype, op.num_cus);
             return launch_gemv_dense(s, op.a, op.a_dtype, op.w, op.c, op.c_dtype, op.N, op.K);
         case OP_GEMV_QUANT:
+            if (op.M == 1 && stream_supported(op.w))
+                return launch_gemv_stream(s, op.a, MVLM_F32, op.w, op.c, MVLM_F32, op.num_cus);
             return launch_gemv_quant(s, (const float*)op.a, op.w, (float*)op.c, op.M, op.N, op.K);
     }
     return hipErrorInvalidValue;
@@ -201,6 +242,11 @@ extern "C" int mvlm_gemv(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, co
                          mvlm_buffer* y, int y_dtype, int N, int K, mvlm_event** ev) {
     const char* fn = __func__;
     RUN(make_gemv(dev, x, x_dtype, W, y, y_dtype, 1, N, K, -1, fn, &op));
+}
+
+extern "C" int mvlm_gemv_grouped(mvlm_device* dev, int count, const mvlm_gemv_desc* descs, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(make_gemv_group(dev, count, descs, fn, &op));
 }
 
 extern "C" int mvlm_gemv_q8_0(mvlm_device* dev, const mvlm_buffer* x, const mvlm_weight* W, mvlm_buffer* y,
@@ -283,6 +329,14 @@ extern "C" int mvlm_plan_add_gemv(mvlm_plan* plan, const mvlm_buffer* x, int x_d
     return st != MVLM_OK ? st : plan_push(plan, op);
 }
 
+extern "C" int mvlm_plan_add_gemv_grouped(mvlm_plan* plan, int count, const mvlm_gemv_desc* descs) {
+    const char* fn = __func__;
+    REQUIRE(plan, "%s: null argument", fn);
+    Op op{};
+    int st = make_gemv_group(plan->dev, count, descs, fn, &op);
+    return st != MVLM_OK ? st : plan_push(plan, op);
+}
+
 extern "C" int mvlm_plan_add_gemm_packed(mvlm_plan* plan, const mvlm_buffer* A, int a_dtype, const mvlm_weight* W,
                                          mvlm_buffer* C, int c_dtype, int M) {
     const char* fn = __func__;
@@ -351,19 +405,24 @@ extern "C" int mvlm_plan_profile(mvlm_plan* plan, float* op_ms, int capacity) {
     REQUIRE(plan && op_ms, "mvlm_plan_profile: null argument");
     const int n = (int)plan->ops.size();
     REQUIRE(capacity >= n, "mvlm_plan_profile: capacity %d below the plan size %d", capacity, n);
-    std::vector<hipEvent_t> marks(n + 1, nullptr);
+    // two events per launch, attached to the kernel's own dispatch packet
+    std::vector<hipEvent_t> ev(2 * (size_t)n, nullptr);
     int st = MVLM_OK;
-    for (int i = 0; i <= n && st == MVLM_OK; ++i) st = check_hip(hipEventCreate(&marks[i]), "hipEventCreate");
+    for (size_t i = 0; i < ev.size() && st == MVLM_OK; ++i) st = check_hip(hipEventCreate(&ev[i]), "hipEventCreate");
     hipStream_t s = plan->dev->stream;
-    if (st == MVLM_OK) st = check_hip(hipEventRecord(marks[0], s), "hipEventRecord");
+    KernelTiming& t = kernel_timing();
     for (int i = 0; i < n && st == MVLM_OK; ++i) {
+        t.start = ev[2 * i];
+        t.stop = ev[2 * i + 1];
         hipError_t e = enqueue_op(s, plan->ops[i]);
-        st = (e == hipSuccess) ? check_hip(hipEventRecord(marks[i + 1], s), "hipEventRecord") : check_hip(e, "plan launch");
+        t = KernelTiming{};
+        if (e != hipSuccess) st = check_hip(e, "plan launch");
     }
-    if (st == MVLM_OK) st = check_hip(hipEventSynchronize(marks[n]), "hipEventSynchronize");
+    t = KernelTiming{};
+    if (st == MVLM_OK && n > 0) st = check_hip(hipEventSynchronize(ev[2 * (size_t)n - 1]), "hipEventSynchronize");
     for (int i = 0; i < n && st == MVLM_OK; ++i)
-        st = check_hip(hipEventElapsedTime(&op_ms[i], marks[i], marks[i + 1]), "hipEventElapsedTime");
-    for (hipEvent_t e : marks)
+        st = check_hip(hipEventElapsedTime(&op_ms[i], ev[2 * i], ev[2 * i + 1]), "hipEventElapsedTime");
+    for (hipEvent_t e : ev)
         if (e) (void)hipEventDestroy(e);
     return st;
 }

@@ -11,6 +11,11 @@ namespace mvlm {
 
 static thread_local std::string g_last_error;
 
+KernelTiming& kernel_timing() {
+    static thread_local KernelTiming t;
+    return t;
+}
+
 static bool quiet() {
     static int q = -1;
     if (q < 0) {

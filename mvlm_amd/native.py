@@ -13,7 +13,7 @@ from ctypes import POINTER, byref, c_char_p, c_double, c_float, c_int, c_int64, 
 import numpy as np
 
 PKG = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PKG, "lib", "libmvlm_hip.so")
+LIB_PATH = os.environ.get("MVLM_LIB_PATH") or os.path.join(PKG, "lib", "libmvlm_hip.so")
 
 F32, F16, Q4_0, Q8_0, BF16 = 0, 1, 2, 8, 30
 LAYOUT_NK, LAYOUT_KN = 0, 1
@@ -37,6 +37,12 @@ class DeviceInfo(ctypes.Structure):
                 ("global_mem_size", c_uint64), ("local_mem_size", c_uint64), ("l2_cache_size", c_uint64),
                 ("peak_hbm_gbs", c_double), ("peak_fp16_tflops", c_double)]
 
+
+class GemvDesc(ctypes.Structure):
+    _fields_ = [("x", c_void_p), ("x_dtype", c_int), ("W", c_void_p), ("y", c_void_p), ("y_dtype", c_int)]
+
+
+MAX_GROUP = 8
 
 _P = c_void_p
 _PP = POINTER(c_void_p)
@@ -71,6 +77,8 @@ _SIGNATURES = {
     "mvlm_gemm_tiled": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _PP]),
     "mvlm_gemm_packed": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, c_int, c_int, _PP]),
     "mvlm_gemv": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, c_int, _PP]),
+    "mvlm_gemv_grouped": (c_int, [_P, c_int, POINTER(GemvDesc), _PP]),
+    "mvlm_plan_add_gemv_grouped": (c_int, [_P, c_int, POINTER(GemvDesc)]),
     "mvlm_gemv_q8_0": (c_int, [_P, _P, _P, _P, c_int, c_int, _PP]),
     "mvlm_gemv_q4_0": (c_int, [_P, _P, _P, _P, c_int, c_int, _PP]),
     "mvlm_gemm_q8_0": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _PP]),
@@ -237,6 +245,13 @@ def _ev(want: bool):
     return (c_void_p(), True) if want else (None, False)
 
 
+def _descs(entries):
+    arr = (GemvDesc * max(1, len(entries)))()
+    for i, (x, xd, W, y, yd) in enumerate(entries):
+        arr[i] = GemvDesc(x.handle, xd, W.handle, y.handle, yd)
+    return arr
+
+
 class Plan:
     """A recorded launch sequence run from native code (eagerly or as a HIP graph).
     Keeps references to the buffers and weights it names so they outlive it."""
@@ -254,6 +269,14 @@ class Plan:
     def add_gemv(self, x, x_dtype, W, y, y_dtype, M=1):
         _call("mvlm_plan_add_gemv", self.handle, x.handle, x_dtype, W.handle, y.handle, y_dtype, M)
         self._keep += [x, W, y]
+        return self
+
+    def add_gemv_grouped(self, entries):
+        """entries: [(x, x_dtype, W, y, y_dtype), ...] served by one launch."""
+        arr = _descs(entries)
+        _call("mvlm_plan_add_gemv_grouped", self.handle, len(entries), arr)
+        for x, _, W, y, _ in entries:
+            self._keep += [x, W, y]
         return self
 
     def add_gemm_packed(self, A, a_dtype, W, C, c_dtype, M):
@@ -370,6 +393,10 @@ class Device:
 
     def gemv(self, x, x_dtype, W, y, y_dtype, N, K, event=False):
         return self._launch("mvlm_gemv", (x.handle, x_dtype, W.handle, y.handle, y_dtype, N, K), event)
+
+    def gemv_grouped(self, entries, event=False):
+        """entries: [(x, x_dtype, W, y, y_dtype), ...], one launch for all."""
+        return self._launch("mvlm_gemv_grouped", (len(entries), _descs(entries)), event)
 
     def gemv_q8_0(self, x, W, y, N, K, event=False):
         return self._launch("mvlm_gemv_q8_0", (x.handle, W.handle, y.handle, N, K), event)

@@ -175,7 +175,8 @@ def test_dequant_known_answer_blocks(dev):
         assert np.array_equal(W.dequant().ravel().view(np.uint32), np.array(case["bits"], np.uint32)), case["name"]
 
 
-QSHAPES = [(6144, 2048), (2048, 8192), (1, 32), (37, 96), (8192, 2048)]
+QSHAPES = [(6144, 2048), (2048, 8192), (1, 32), (37, 96), (8192, 2048), (3456, 1152), (51200, 2048),
+           (24, 20480), (5, 64)]
 
 
 @pytest.mark.parametrize("qt", [Q8, Q4])
@@ -366,3 +367,68 @@ def test_event_timing(dev, orc):
     t = ctypes.c_float()
     native.check(native.lib().mvlm_marker_elapsed_ms(m0.handle, m1.handle, ctypes.byref(t)), "marker")
     assert t.value > 0.0
+
+
+# ---------------------------------------------------------------------------
+# grouped decode GEMV (independent projections of one Phi-1.5 block, one launch)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("qt", [Q8, Q4])
+def test_gemv_grouped_phi_block(dev, orc, qt):
+    """QKV + fc1 share the block input; dense + fc2 read the attention / MLP branches."""
+    shapes = [(6144, 2048, 0), (8192, 2048, 0), (2048, 2048, 1), (2048, 8192, 2)]
+    xs_host = [orc.normal_f32(2048, 191), orc.normal_f32(2048, 192), orc.normal_f32(8192, 193)]
+    xs = [dev.upload(v) for v in xs_host]
+    blocks = [make_quant(orc, qt, N, K, 194 + i) for i, (N, K, _) in enumerate(shapes)]
+    Ws = [dev.pack(b, qt, N, K) for b, (N, K, _) in zip(blocks, shapes)]
+    ys = [dev.alloc(N * 4) for N, _, _ in shapes]
+    ys1 = [dev.alloc(N * 4) for N, _, _ in shapes]
+    dev.gemv_grouped([(xs[xi], F32, W, y, F32) for (N, K, xi), W, y in zip(shapes[:2], Ws[:2], ys[:2])])
+    dev.gemv_grouped([(xs[xi], F32, W, y, F32) for (N, K, xi), W, y in zip(shapes[2:], Ws[2:], ys[2:])])
+    kind = "q8_0" if qt == Q8 else "q4_0"
+    deq = orc.dequant_q8_0 if qt == Q8 else orc.dequant_q4_0
+    for (N, K, xi), W, b, y, y1 in zip(shapes, Ws, blocks, ys, ys1):
+        dev.gemv(xs[xi], F32, W, y1, F32, N, K)
+        got = y.download(np.float32)
+        assert np.array_equal(got, y1.download(np.float32))      # same kernel, same bits
+        ref = orc.gemm_nk(kind, xs_host[xi], b, 1, N, K)[0]
+        _, S = orc.gemm_f64(xs_host[xi].astype(np.float64)[None], deq(b).astype(np.float64).reshape(N, K), 1, N, K)
+        ok, worst = within(got, ref, S[0], 1e-5)
+        assert ok, (N, K, worst)
+
+
+def test_gemv_grouped_dense_and_plan(dev, orc):
+    shapes = [(300, 512), (77, 1024), (1, 64)]
+    xs_host = [orc.normal_f16(K, 201 + i) for i, (_, K) in enumerate(shapes)]
+    Wh = [orc.normal_f16(N * K, 211 + i, 0.02) for i, (N, K) in enumerate(shapes)]
+    xs = [dev.upload(v) for v in xs_host]
+    Ws = [dev.pack(w, F16, N, K) for w, (N, K) in zip(Wh, shapes)]
+    ys = [dev.alloc(N * 4) for N, _ in shapes]
+    plan = m.Plan(dev)
+    plan.add_gemv_grouped([(x, F16, W, y, F32) for x, W, y in zip(xs, Ws, ys)])
+    plan.use_graph(True)
+    plan.run(3)
+    dev.sync()
+    for (N, K), xh, wh, y in zip(shapes, xs_host, Wh, ys):
+        ref, S = orc.gemm_f64(orc.f16_to_f32(xh).astype(np.float64)[None],
+                              orc.f16_to_f32(wh).astype(np.float64).reshape(N, K), 1, N, K)
+        ok, worst = within(y.download(np.float32), ref[0], S[0], 1e-3)
+        assert ok, worst
+
+
+def test_gemv_grouped_errors(dev):
+    from mvlm_amd import native
+    x, y = dev.alloc(4 * 65536), dev.alloc(4 * 4096)
+    W8 = dev.pack(np.zeros(34 * 64, np.uint8), Q8, 64, 1024)
+    W4 = dev.pack(np.zeros(18 * 64, np.uint8), Q4, 64, 1024)
+    with pytest.raises(native.MvlmError) as e:           # mixed weight formats
+        dev.gemv_grouped([(x, F32, W8, y, F32), (x, F32, W4, y, F32)])
+    assert e.value.code == native.ERR_INVALID_ARG
+    with pytest.raises(native.MvlmError) as e:           # more than MVLM_MAX_GROUP entries
+        dev.gemv_grouped([(x, F32, W8, y, F32)] * 9)
+    assert e.value.code == native.ERR_INVALID_ARG
+    Wlong = dev.pack(np.zeros(34 * 2048, np.uint8), Q8, 1, 65536)   # 64 KiB rows
+    with pytest.raises(native.MvlmError) as e:
+        dev.gemv_grouped([(x, F32, Wlong, y, F32)])
+    assert e.value.code == native.ERR_UNSUPPORTED
+    dev.gemv(x, F32, Wlong, y, F32, 1, 65536)            # the single entry point still serves it
