@@ -139,7 +139,7 @@ inline int64_t weight_row_bytes(const mvlm_weight* w) { return is_dense(w->dtype
 hipError_t launch_gemm_mfma(hipStream_t s, const void* A, int ab_dtype, const void* B, void* C,
                             int c_dtype, int batch, int M, int N, int K, int64_t lda, int64_t ldb,
                             int64_t ldc, int64_t strideA, int64_t strideB, int64_t strideC,
-                            int num_cus);
+                            int kread_b, int num_cus);
 hipError_t launch_pack(hipStream_t s, const void* src, int dtype, int layout, int N, int K,
                        mvlm_weight* w);
 hipError_t launch_dequant(hipStream_t s, const mvlm_weight* w, float* out);

@@ -26,6 +26,7 @@ struct Op {
     int a_dtype = MVLM_F16, c_dtype = MVLM_F32;
     int batch = 1, M = 0, N = 0, K = 0;
     int64_t lda = 0, ldb = 0, ldc = 0, sA = 0, sB = 0, sC = 0;
+    int kread_b = 0;              // B rows readable (zero padded) up to this K
     int num_cus = 256;
     // grouped GEMV
     int gcount = 0;
@@ -81,6 +82,7 @@ int make_gemm_packed(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, const 
     op->a_dtype = a_dtype; op->c_dtype = c_dtype;
     op->M = M; op->N = N; op->K = K;
     op->lda = K; op->ldb = W->ld; op->ldc = N;
+    op->kread_b = (int)W->ld;     // packed rows are zero padded to ld = roundup(K, 64)
     op->num_cus = dev->prop.multiProcessorCount;
     return MVLM_OK;
 }
@@ -105,6 +107,7 @@ int make_gemm_batched(mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer*
     op->a_dtype = MVLM_F16; op->c_dtype = MVLM_F32;
     op->batch = batch; op->M = M; op->N = N; op->K = K;
     op->lda = lda; op->ldb = ldb; op->ldc = ldc; op->sA = sA; op->sB = sB; op->sC = sC;
+    op->kread_b = K;
     op->num_cus = dev->prop.multiProcessorCount;
     return MVLM_OK;
 }
@@ -177,7 +180,7 @@ hipError_t enqueue_op(hipStream_t s, const Op& op) {
             return launch_gemm_tiled(s, (const uint16_t*)op.a, (const uint16_t*)op.b, (uint16_t*)op.c, op.M, op.N, op.K);
         case OP_GEMM_MFMA:
             return launch_gemm_mfma(s, op.a, op.a_dtype, op.b, op.c, op.c_dtype, op.batch, op.M, op.N, op.K,
-                                    op.lda, op.ldb, op.ldc, op.sA, op.sB, op.sC, op.num_cus);
+                                    op.lda, op.ldb, op.ldc, op.sA, op.sB, op.sC, op.kread_b, op.num_cus);
         case OP_GEMV_DENSE:
             if (stream_supported(op.w))
                 return launch_gemv_stream(s, op.a, op.a_dtype, op.w, op.c, op.c_dtype, op.num_cus);
