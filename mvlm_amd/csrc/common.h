@@ -134,7 +134,7 @@ bool stream_supported(const mvlm_weight* w);
 hipError_t launch_gemv_stream(hipStream_t s, const void* x, int x_dtype, const mvlm_weight* W, void* y,
                               int y_dtype, int num_cus);
 hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const* xs, int x_dtype,
-                                    const mvlm_weight* const* ws, void* const* ys, const int* y_dtypes);
+                                    const mvlm_weight* const* ws, void* const* ys, const int* y_dtypes, int num_cus);
 inline int64_t weight_row_bytes(const mvlm_weight* w) { return is_dense(w->dtype) ? w->ld * (int64_t)dtype_size(w->dtype) : w->ld; }
 hipError_t launch_gemm_mfma(hipStream_t s, const void* A, int ab_dtype, const void* B, void* C,
                             int c_dtype, int batch, int M, int N, int K, int64_t lda, int64_t ldb,

@@ -38,16 +38,19 @@ template <typename WT>
 struct DenseFmt {
     static constexpr int WPL = 16 / (int)sizeof(WT);   // weights per lane per chunk
     static constexpr bool QUANT = false;
+    static constexpr int MIN_WAVES = 8;                // per SIMD: 4 blocks of 8 waves per CU
 };
 
 struct Q8Fmt {
     static constexpr int WPL = 16;
     static constexpr bool QUANT = true;
+    static constexpr int MIN_WAVES = 8;
 };
 
 struct Q4Fmt {
     static constexpr int WPL = 32;
     static constexpr bool QUANT = true;
+    static constexpr int MIN_WAVES = 4;                // 32 x values per lane need more registers
 };
 
 // x values of one chunk as raw bits: E elements of XT in XD dwords.
@@ -56,23 +59,6 @@ struct XRaw {
     static constexpr int XD = E * (int)sizeof(XT) / 4;
     uint32_t d[XD];
 };
-
-// Vector loads of E consecutive x elements at k (caller keeps k + E <= K).
-template <typename XT, int E>
-__device__ __forceinline__ void load_x_raw(const XT* __restrict__ x, int k, XRaw<XT, E>& out) {
-    constexpr int XD = XRaw<XT, E>::XD;
-    const uint32_t* p = reinterpret_cast<const uint32_t*>(x + k);
-    if constexpr (XD % 4 == 0) {
-#pragma unroll
-        for (int v = 0; v < XD / 4; ++v) {
-            u32x4 u = *reinterpret_cast<const u32x4*>(p + 4 * v);
-            out.d[4 * v + 0] = u[0]; out.d[4 * v + 1] = u[1]; out.d[4 * v + 2] = u[2]; out.d[4 * v + 3] = u[3];
-        }
-    } else {   // XD == 2: four 16-bit elements
-        u32x2 u = *reinterpret_cast<const u32x2*>(p);
-        out.d[0] = u[0]; out.d[1] = u[1];
-    }
-}
 
 template <typename XT, int E>
 __device__ __forceinline__ float x_at(const XRaw<XT, E>& r, int j) {
@@ -124,6 +110,45 @@ __device__ __forceinline__ float chunk_dot(Q4Fmt, u32x4 q, uint16_t dh, const XR
 }
 
 
+// ---- LDS staging -------------------------------------------------------------
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// A lane's x values for one chunk are XB = WPL * sizeof(XT) consecutive bytes
+// (8 .. 128).  Read from LDS as 16-byte slots, lane l reads slot SL*l + i in
+// its i-th read; 16 lanes share one LDS cycle, so with SL > 1 lanes l and
+// l + 16/SL would hit the same banks.  x is therefore stored with its 16-byte
+// slot s at s ^ ((s >> 4) & (SL - 1)) (a permutation inside each 256-byte
+// group, its own inverse), which gives the 16 lanes of a read 16 distinct
+// bank groups.
+template <int SL>
+__device__ __forceinline__ int x_slot(int s) { return s ^ ((s >> 4) & (SL - 1)); }
+
+// Copy nbytes (a multiple of W = 4 or 16) from global src into LDS dst with
+// direct W-byte loads; the waves of the block take pieces of 64*W bytes in
+// turn.  With SL > 1 the 16-byte slots are permuted by x_slot.  Source reads
+// are clamped to [0, nbytes - W]: bytes landing beyond nbytes are never read,
+// and the LDS region is rounded up to whole pieces.
+template <int W, int SL, int NW>
+__device__ __forceinline__ void stage_to_lds(uint8_t* dst, const uint8_t* __restrict__ src, int nbytes,
+                                             int wave, int lane) {
+    static_assert(W == 4 || W == 16, "direct load width");
+    for (int piece = wave; piece * 64 * W < nbytes; piece += NW) {
+        const int phys = piece * 64 * W + lane * W;
+        const int logical = x_slot<SL>(phys >> 4) * 16 + (phys & 15);
+        const uint8_t* from = src + min(logical, nbytes - W);
+        if constexpr (W == 16) __builtin_amdgcn_global_load_lds(from, (lds_void*)(dst + piece * 64 * W), 16, 0, 0);
+        else __builtin_amdgcn_global_load_lds(from, (lds_void*)(dst + piece * 64 * W), 4, 0, 0);
+    }
+}
+
+// s_waitcnt with vmcnt = n and expcnt / lgkmcnt unconstrained (gfx9 encoding)
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // ---- the kernel ------------------------------------------------------------
 
 // One problem of a grouped launch.  Chunk c of a row covers bytes
@@ -138,157 +163,263 @@ struct StreamProblem {
     const uint16_t* scales;
     void* y;
     int64_t ld_bytes;
-    int N, K, y_dtype, split;
+    int N, K, y_dtype;
+    int shape;                     // index into kShapes
+    int rows_per_block;            // block j owns rows [j*rows_per_block, (j+1)*rows_per_block) below N
     int block_begin;               // first block of this problem in the grid
 };
 
 constexpr int MAX_GROUP = 8;
+constexpr int NWAVE = 8;           // waves per block
 
 struct StreamGroup {
     StreamProblem p[MAX_GROUP];
     int count;
 };
 
-template <class F, typename XT, int R, int CW>
-__global__ __launch_bounds__(256) void gemv_stream_kernel(const StreamGroup g) {
+// Work shape of one wave by row length in 1 KiB chunks: R rows x CW chunks,
+// the row split over SPLIT waves when it is longer than CW chunks.  A wave
+// keeps 4 to 8 loads of 16 bytes per lane in flight; whole rows per wave
+// (SPLIT = 1) need no combine step.
+struct Shape { int max_chunks, R, CW, SPLIT; };
+constexpr Shape kShapes[] = {{1, 4, 1, 1}, {2, 2, 2, 1}, {4, 1, 4, 1}, {8, 1, 4, 2}, {16, 1, 8, 2}};
+constexpr int kNumShapes = 5;
+static_assert(sizeof(kShapes) / sizeof(kShapes[0]) == kNumShapes, "one kernel case per shape");
+
+// The rows [row0, row0 + R) of one wave (those below the block's end rb1),
+// its chunks wsub*CW ... of each.
+// x and the scales are already being staged into LDS (staging loads were
+// issued before these and complete first).
+template <class F, typename XT, int R, int CW, int SPLIT>
+__device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int rb1, int64_t s_base, int x_region,
+                                            const uint8_t* lds, float (*part)[4], int wave, int lane) {
     constexpr int WPL = F::WPL;
-    int pi = 0;
+    constexpr int XB = WPL * (int)sizeof(XT);        // x bytes per lane per chunk
+    constexpr int SL = XB >= 16 ? XB / 16 : 1;       // 16-byte LDS slots per lane per chunk
+    const int N = P.N, K = P.K, nb = K >> 5;
+    const int wsub = wave % SPLIT;
+    const int row0 = rb0 + (wave / SPLIT) * R;
+    const bool active = row0 < rb1;
+
+    // the codes: every load of this wave before any arithmetic
+    const uint8_t* rowp[R];
+    int srow[R];                                      // row's scale byte offset in the staged region
 #pragma unroll
-    for (int i = 1; i < MAX_GROUP; ++i)
-        if (i < g.count && (int)blockIdx.x >= g.p[i].block_begin) pi = i;
-    const StreamProblem& P = g.p[pi];
-    const XT* __restrict__ x = (const XT*)P.x;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int split = P.split, N = P.N, K = P.K;
-    const int wsub = wave % split;
-    const int row0 = (((int)blockIdx.x - P.block_begin) * (4 / split) + wave / split) * R;
-    const int nb = K >> 5;
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = (int64_t)min(row0 + r, rb1 - 1);
+        rowp[r] = P.codes + row * P.ld_bytes;
+        srow[r] = (int)(row * (nb * 2) - s_base);
+    }
+    u32x4 q[R][CW];
+    int kk[CW];
+    bool valid[CW];
+#pragma unroll
+    for (int i = 0; i < CW; ++i) {
+        const int c = wsub * CW + i;
+        const int k = (64 * c + lane) * WPL;
+        valid[i] = active && k < K;
+        kk[i] = k < K ? k : 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            q[r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rowp[r] + (int64_t)kk[i] * 16 / WPL));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // staging done for every wave -> x and scales from LDS, chunk by chunk
+    wait_vmcnt<R * CW>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-
-    if (row0 < N) {
-        const uint8_t* rowp[R];
-        const uint16_t* rows_s[R];
+#pragma unroll
+    for (int i = 0; i < CW; ++i) {
+        XRaw<XT, WPL> xr;
+        const int xbyte = kk[i] * (int)sizeof(XT);
+        if constexpr (XB >= 16) {
+#pragma unroll
+            for (int v = 0; v < SL; ++v) {
+                const u32x4 u = reinterpret_cast<const u32x4*>(lds)[x_slot<SL>((xbyte >> 4) + v)];
+                xr.d[4 * v + 0] = u[0]; xr.d[4 * v + 1] = u[1];
+                xr.d[4 * v + 2] = u[2]; xr.d[4 * v + 3] = u[3];
+            }
+        } else {   // XB == 8
+            const u32x2 u = *reinterpret_cast<const u32x2*>(lds + xbyte);
+            xr.d[0] = u[0]; xr.d[1] = u[1];
+        }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int64_t row = (int64_t)min(row0 + r, N - 1);
-            rowp[r] = P.codes + row * P.ld_bytes;
-            rows_s[r] = P.scales + row * nb;
+            uint16_t dh = 0;
+            if constexpr (F::QUANT) dh = *reinterpret_cast<const uint16_t*>(lds + x_region + srow[r] + (kk[i] >> 5) * 2);
+            const float v = chunk_dot(F{}, q[r][i], dh, xr, acc[r]);
+            acc[r] = valid[i] ? v : acc[r];
         }
-        u32x4 q[R][CW];
-        uint16_t dh[R][CW];
-        XRaw<XT, WPL> xr[CW];
-        bool valid[CW];
-        // 1) every load of this wave is issued before any arithmetic
-#pragma unroll
-        for (int i = 0; i < CW; ++i) {
-            const int c = wsub * CW + i;
-            const int k = (64 * c + lane) * WPL;
-            valid[i] = k < K;
-            const int kk = valid[i] ? k : 0;   // byte offset in the row: kk * 16 / WPL
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                q[r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rowp[r] + (int64_t)kk * 16 / WPL));
-                if constexpr (F::QUANT) dh[r][i] = rows_s[r][kk >> 5];
-                else dh[r][i] = 0;
-            }
-            load_x_raw<XT, WPL>(x, kk, xr[i]);
-        }
-        // 2) convert and accumulate
-#pragma unroll
-        for (int i = 0; i < CW; ++i)
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                float v = chunk_dot(F{}, q[r][i], dh[r][i], xr[i], acc[r]);
-                acc[r] = valid[i] ? v : acc[r];
-            }
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
 
-    if (split == 1) {                      // uniform over the block
-        if (lane == 0 && row0 < N) {
+    if constexpr (SPLIT == 1) {
+        if (lane == 0 && active) {
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                if (row0 + r < N) store_out(P.y, row0 + r, acc[r], P.y_dtype);
+                if (row0 + r < rb1) store_out(P.y, row0 + r, acc[r], P.y_dtype);
         }
     } else {
-        __shared__ float part[4][R];
         if (lane == 0) {
 #pragma unroll
             for (int r = 0; r < R; ++r) part[wave][r] = acc[r];
         }
         __syncthreads();
-        if (wsub == 0 && lane == 0 && row0 < N) {
+        if (wsub == 0 && lane == 0 && active) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 float v = part[wave][r];
-                for (int s = 1; s < split; ++s) v += part[wave + s][r];
-                if (row0 + r < N) store_out(P.y, row0 + r, v, P.y_dtype);
+#pragma unroll
+                for (int s = 1; s < SPLIT; ++s) v += part[wave + s][r];
+                if (row0 + r < rb1) store_out(P.y, row0 + r, v, P.y_dtype);
             }
         }
     }
 }
 
-// ---- launch configuration ----------------------------------------------------
+// A block of NWAVE waves owns a contiguous range of at most R * NWAVE / SPLIT
+// rows of one problem.
+// Per block, x and the rows' block scales are staged in LDS once (direct
+// global->LDS loads), so each x element crosses the L2->CU path once per
+// block rather than once per wave; the weight codes go straight to
+// registers.  Issue order: x and scale staging, then every code load, then
+// the wait for the staging alone (vmcnt counts in issue order), the block
+// barrier, the LDS reads, and the wait for the codes.
+template <class F, typename XT>
+__global__ __launch_bounds__(64 * NWAVE, F::MIN_WAVES) void gemv_stream_kernel(const StreamGroup g) {
+    constexpr int XB = F::WPL * (int)sizeof(XT);
+    constexpr int SL = XB >= 16 ? XB / 16 : 1;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ float part[NWAVE][4];
 
-// Rows per wave and chunks per wave for each format: R * CW = 4 loads of
-// 16 bytes per lane.  A Q8_0 row of K = 2048 is 2 chunks (R = 2 rows per
-// wave), a Q4_0 row of K = 2048 is 1 chunk (R = 4).  Rows per wave (Q8_0),
-// measured on MI355X over the grouped Phi-1.5 decode step:
-// R = 1: 599 us, 2: 428 us, 4: 439 us, 8: 470 us per step.
-#ifndef MVLM_STREAM_R
-#define MVLM_STREAM_R 2
-#endif
-template <class F> struct StreamShape { static constexpr int R = MVLM_STREAM_R, CW = 2; };
-template <> struct StreamShape<Q4Fmt> { static constexpr int R = 2 * MVLM_STREAM_R, CW = 1; };
+    int pi = 0;
+#pragma unroll
+    for (int i = 1; i < MAX_GROUP; ++i)
+        if (i < g.count && (int)blockIdx.x >= g.p[i].block_begin) pi = i;
+    const StreamProblem& P = g.p[pi];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int N = P.N, K = P.K, nb = K >> 5;
+    const int rb0 = ((int)blockIdx.x - P.block_begin) * P.rows_per_block;
+    const int rb1 = min(rb0 + P.rows_per_block, N);
+
+    // stage x (and the block's scales) in LDS
+    // (x_bytes is a multiple of XB, so of 16 when XB >= 16)
+    const int x_bytes = K * (int)sizeof(XT);
+    const int x_region = (x_bytes + 1023) & ~1023;
+    stage_to_lds<(XB >= 16 ? 16 : 4), SL, NWAVE>(lds, (const uint8_t*)P.x, x_bytes, wave, lane);
+    int64_t s_base = 0;                               // global byte offset of the first staged scale byte
+    if constexpr (F::QUANT) {
+        const int64_t s_begin = (int64_t)rb0 * (nb * 2);
+        const int64_t s_end = (int64_t)rb1 * (nb * 2);
+        s_base = s_begin & ~(int64_t)15;
+        const int s_bytes = (int)((s_end - s_base + 15) & ~(int64_t)15);
+        stage_to_lds<16, 1, NWAVE>(lds + x_region, (const uint8_t*)P.scales + s_base, s_bytes, wave, lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    switch (P.shape) {   // uniform over the block
+#define MVLM_SHAPE_CASE(i)                                                                               \
+    case i:                                                                                              \
+        stream_rows<F, XT, kShapes[i].R, kShapes[i].CW, kShapes[i].SPLIT>(P, rb0, rb1, s_base, x_region, \
+                                                                           lds, part, wave, lane);       \
+        break;
+        MVLM_SHAPE_CASE(0) MVLM_SHAPE_CASE(1) MVLM_SHAPE_CASE(2) MVLM_SHAPE_CASE(3) MVLM_SHAPE_CASE(4)
+#undef MVLM_SHAPE_CASE
+    }
+}
+
+// ---- launch configuration ----------------------------------------------------
 
 static int weight_wpl(int dtype) {
     return dtype == MVLM_Q8_0 ? 16 : dtype == MVLM_Q4_0 ? 32 : 16 / (int)dtype_size(dtype);
 }
-static int shape_cw(int dtype) { return dtype == MVLM_Q4_0 ? 1 : 2; }
-static int shape_r(int dtype) { return dtype == MVLM_Q4_0 ? 2 * MVLM_STREAM_R : MVLM_STREAM_R; }
 
-// waves sharing one row: ceil(chunks per row / CW), rounded up to 1, 2 or 4
-static int stream_split(const mvlm_weight* w) {
+// index into kShapes for this weight's row length, -1 if rows are too long
+static int stream_shape(const mvlm_weight* w) {
     const int64_t chunks = (weight_row_bytes(w) + 1023) / 1024;
-    const int cw = shape_cw(w->dtype);
-    const int64_t s = (chunks + cw - 1) / cw;
-    return s <= 1 ? 1 : s <= 2 ? 2 : s <= 4 ? 4 : 0;
+    for (int i = 0; i < kNumShapes; ++i)
+        if (chunks <= kShapes[i].max_chunks) return i;
+    return -1;
 }
 
+static int rows_per_block(int shape) { return kShapes[shape].R * (NWAVE / kShapes[shape].SPLIT); }
+
+// LDS bytes of one block: x, then the block's scales plus the alignment
+// slack of their start, each rounded to the 1 KiB pieces the staging writes.
+// Scale reads reach up to 15 bytes past the scale array, which the weight
+// allocation pads.
+static size_t stream_lds_bytes(const mvlm_weight* w, int x_dtype, int shape) {
+    const size_t x_bytes = (size_t)w->K * dtype_size(x_dtype);
+    size_t bytes = (x_bytes + 1023) & ~(size_t)1023;
+    if (is_quant(w->dtype))
+        bytes += ((size_t)rows_per_block(shape) * (size_t)(w->K / 32) * 2 + 30 + 1023) & ~(size_t)1023;
+    return bytes;
+}
+
+constexpr size_t STREAM_LDS_MAX = 152 * 1024;
+
 bool stream_supported(const mvlm_weight* w) {
-    return stream_split(w) > 0 && w->K % weight_wpl(w->dtype) == 0;
+    const int shape = stream_shape(w);
+    return shape >= 0 && w->K % weight_wpl(w->dtype) == 0 && stream_lds_bytes(w, MVLM_F32, shape) <= STREAM_LDS_MAX;
 }
 
 int stream_max_group() { return MAX_GROUP; }
 
+// Blocks per launch: each problem gets the fewest blocks whose row slots hold
+// its rows.  (Spreading a problem over more, part-filled blocks to even out
+// the bytes per CU was measured slower on MI355X: every block stages all of
+// x, so x traffic grows with the block count, and part-filled blocks idle
+// waves.  Computing block bounds by division, even once per block, also cost
+// ~0.2 us per launch.)
+static unsigned partition(StreamGroup& g) {
+    unsigned begin = 0;
+    for (int i = 0; i < g.count; ++i) {
+        StreamProblem& p = g.p[i];
+        p.rows_per_block = rows_per_block(p.shape);
+        p.block_begin = (int)begin;
+        begin += (unsigned)((p.N + p.rows_per_block - 1) / p.rows_per_block);
+    }
+    return begin;
+}
+
 template <class F, typename XT>
-static hipError_t launch_group(hipStream_t s, const StreamGroup& g, unsigned blocks) {
-    launch_kernel(gemv_stream_kernel<F, XT, StreamShape<F>::R, StreamShape<F>::CW>, dim3(blocks), dim3(256), 0, s, g);
+static hipError_t launch_group(hipStream_t s, StreamGroup& g, size_t lds) {
+    auto kernel = gemv_stream_kernel<F, XT>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)STREAM_LDS_MAX);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const unsigned blocks = partition(g);
+    launch_kernel(kernel, dim3(blocks), dim3(64 * NWAVE), (uint32_t)lds, s, g);
     return hipGetLastError();
 }
 
 template <class F>
-static hipError_t launch_group_x(hipStream_t s, int x_dtype, const StreamGroup& g, unsigned blocks) {
+static hipError_t launch_group_x(hipStream_t s, int x_dtype, StreamGroup& g, size_t lds) {
     switch (x_dtype) {
-        case MVLM_F32: return launch_group<F, float>(s, g, blocks);
-        case MVLM_F16: return launch_group<F, __half>(s, g, blocks);
-        case MVLM_BF16: return launch_group<F, __hip_bfloat16>(s, g, blocks);
+        case MVLM_F32: return launch_group<F, float>(s, g, lds);
+        case MVLM_F16: return launch_group<F, __half>(s, g, lds);
+        case MVLM_BF16: return launch_group<F, __hip_bfloat16>(s, g, lds);
         default: return hipErrorInvalidValue;
     }
 }
 
 // All problems share the weight dtype and x dtype (checked by the caller).
 hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const* xs, int x_dtype,
-                                    const mvlm_weight* const* ws, void* const* ys, const int* y_dtypes) {
+                                    const mvlm_weight* const* ws, void* const* ys, const int* y_dtypes, int num_cus) {
     if (count < 1 || count > MAX_GROUP) return hipErrorInvalidValue;
     StreamGroup g{};
     g.count = count;
     const int dtype = ws[0]->dtype;
-    const int R = shape_r(dtype);
-    unsigned blocks = 0;
+    size_t lds = 0;
     for (int i = 0; i < count; ++i) {
         const mvlm_weight* w = ws[i];
         StreamProblem& p = g.p[i];
@@ -300,24 +431,26 @@ hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const*
         p.N = w->N;
         p.K = w->K;
         p.y_dtype = y_dtypes[i];
-        p.split = stream_split(w);
-        p.block_begin = (int)blocks;
-        const int rows_per_block = R * (4 / p.split);
-        blocks += (unsigned)((w->N + rows_per_block - 1) / rows_per_block);
+        p.shape = stream_shape(w);
+        if (p.shape < 0) return hipErrorInvalidValue;
+        const size_t b = stream_lds_bytes(w, x_dtype, p.shape);
+        lds = b > lds ? b : lds;
     }
+    if (lds > STREAM_LDS_MAX) return hipErrorInvalidValue;
+    (void)num_cus;
     switch (dtype) {
-        case MVLM_Q8_0: return launch_group<Q8Fmt, float>(s, g, blocks);
-        case MVLM_Q4_0: return launch_group<Q4Fmt, float>(s, g, blocks);
-        case MVLM_F32: return launch_group_x<DenseFmt<float>>(s, x_dtype, g, blocks);
-        case MVLM_F16: return launch_group_x<DenseFmt<__half>>(s, x_dtype, g, blocks);
-        case MVLM_BF16: return launch_group_x<DenseFmt<__hip_bfloat16>>(s, x_dtype, g, blocks);
+        case MVLM_Q8_0: return launch_group<Q8Fmt, float>(s, g, lds);
+        case MVLM_Q4_0: return launch_group<Q4Fmt, float>(s, g, lds);
+        case MVLM_F32: return launch_group_x<DenseFmt<float>>(s, x_dtype, g, lds);
+        case MVLM_F16: return launch_group_x<DenseFmt<__half>>(s, x_dtype, g, lds);
+        case MVLM_BF16: return launch_group_x<DenseFmt<__hip_bfloat16>>(s, x_dtype, g, lds);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_gemv_stream(hipStream_t s, const void* x, int x_dtype, const mvlm_weight* W, void* y,
-                              int y_dtype, int /*num_cus*/) {
-    return launch_gemv_stream_group(s, 1, &x, x_dtype, &W, &y, &y_dtype);
+                              int y_dtype, int num_cus) {
+    return launch_gemv_stream_group(s, 1, &x, x_dtype, &W, &y, &y_dtype, num_cus);
 }
 
 }  // namespace mvlm

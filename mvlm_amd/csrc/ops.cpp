@@ -173,7 +173,7 @@ int make_gemv_group(mvlm_device* dev, int count, const mvlm_gemv_desc* descs, co
 hipError_t enqueue_op(hipStream_t s, const Op& op) {
     switch (op.kind) {
         case OP_GEMV_GROUP:
-            return launch_gemv_stream_group(s, op.gcount, op.gx, op.a_dtype, op.gw, op.gy, op.gyd);
+            return launch_gemv_stream_group(s, op.gcount, op.gx, op.a_dtype, op.gw, op.gy, op.gyd, op.num_cus);
         case OP_GEMM_NAIVE:
             return launch_gemm_naive(s, (const uint16_t*)op.a, (const uint16_t*)op.b, (uint16_t*)op.c, op.M, op.N, op.K);
         case OP_GEMM_TILED:
