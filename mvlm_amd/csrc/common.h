@@ -127,8 +127,9 @@ hipError_t launch_gemm_tiled(hipStream_t s, const uint16_t* A, const uint16_t* B
                              int M, int N, int K);
 hipError_t launch_gemv_dense(hipStream_t s, const void* x, int x_dtype, const mvlm_weight* W,
                              void* y, int y_dtype, int N, int K);
-hipError_t launch_gemv_quant(hipStream_t s, const float* X, const mvlm_weight* W, float* Y,
-                             int M, int N, int K);
+// Q8_0 / Q4_0 skinny GEMM on the matrix cores, 1 <= M <= 16 (any row length)
+hipError_t launch_gemm_skinny(hipStream_t s, const float* X, const mvlm_weight* W, float* Y, int M, int N, int K,
+                              int num_cus);
 // M == 1 streaming GEMV for every weight format (rows of at most 16 KiB).
 bool stream_supported(const mvlm_weight* w);
 hipError_t launch_gemv_stream(hipStream_t s, const void* x, int x_dtype, const mvlm_weight* W, void* y,

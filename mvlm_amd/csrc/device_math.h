@@ -72,4 +72,74 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// LDS pointer type of the direct global->LDS loads (global_load_lds_*): lane i
+// of the instruction writes its bytes at base + i * width.
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt with vmcnt = n, expcnt and lgkmcnt unconstrained (gfx9 encoding).
+// Direct LDS loads count in vmcnt like other vector loads, in issue order.
+// (The compiler may strengthen this wait but keeps it; it also adds its own
+// waits for LDS reads it can see.)
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// ---- LDS reads the compiler does not track ------------------------------------
+// The compiler inserts a full vmcnt(0) before any LDS read that may alias an
+// in-flight direct global->LDS load, and merges loop-carried LDS reads into
+// lgkmcnt(0), both of which serialize a software pipeline.  Kernels that
+// manage their own waits read LDS with these inline-asm loads instead, and
+// must then order everything by hand:
+//  * asm_wait_vmcnt<n>() before reading LDS filled by direct loads (and a
+//    barrier when other waves filled it);
+//  * asm_wait_lgkmcnt<n>() and then asm_pin(reg) on each loaded register
+//    before using it, so no use can be scheduled above the wait.  LDS reads
+//    complete in issue order.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+template <int OFF = 0>
+__device__ __forceinline__ u32x4 asm_lds_read_b128(uint32_t addr) {
+    u32x4 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+    return v;
+}
+template <int OFF = 0>
+__device__ __forceinline__ u32x2 asm_lds_read_b64(uint32_t addr) {
+    u32x2 v;
+    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+    return v;
+}
+template <int OFF = 0>
+__device__ __forceinline__ uint32_t asm_lds_read_u16(uint32_t addr) {
+    uint32_t v;
+    asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+    return v;
+}
+// A 16-byte global load the compiler does not track (wait with
+// asm_wait_vmcnt, then asm_pin the result).
+__device__ __forceinline__ u32x4 asm_global_load_b128(const void* p) {
+    u32x4 v;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+template <int n>
+__device__ __forceinline__ void asm_wait_vmcnt() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
+}
+template <int n>
+__device__ __forceinline__ void asm_wait_lgkmcnt() {
+    static_assert(n >= 0 && n < 16, "lgkmcnt range");
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(n) : "memory");
+}
+// Ties a register to the preceding wait: an empty volatile asm that "writes"
+// r, so every use of r is scheduled after the wait.
+template <typename T>
+__device__ __forceinline__ void asm_pin(T& r) {
+    asm volatile("" : "+v"(r));
+}
+
 }  // namespace mvlm

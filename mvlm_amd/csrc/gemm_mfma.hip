@@ -61,15 +61,6 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-// s_waitcnt with vmcnt = n, expcnt and lgkmcnt unconstrained (gfx9 encoding).
-template <int n>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(n >= 0 && n < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 // Direct loads of one operand's stage: ROWS rows starting at tile row r0,
 // K columns [k0, k0+64).  Wave w of NW issues 8-row groups w, w+NW, ...
 template <int ROWS, int NW>
@@ -234,6 +225,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(const GemmArg
             mma(f[ks & 1]);
             __builtin_amdgcn_sched_barrier(0);
         }
+        // The next stage's first fragments (read during the last k-step) have
+        // had a whole k-step of MFMAs to land.  Waiting for them here leaves no
+        // LDS read pending across the loop back-edge; otherwise the compiler's
+        // wait insertion merges the entry and back-edge states and puts a full
+        // lgkmcnt(0) in front of the first MFMA of every stage, after the next
+        // k-step's reads have been issued.
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
     }
 
     const int64_t c_off = (int64_t)blockIdx.z * p.sC;

@@ -1,0 +1,321 @@
+// Dequantizing skinny GEMM over GGUF Q8_0 / Q4_0 weights on the matrix cores:
+// Y[m][n] = sum_k X[m][k] * w(n, k), 1 <= M <= 16, X and Y fp32 row-major.
+//
+// The reference plans this kernel (README.md:57, PLAN.md:65) but never wrote
+// it.  With M > 1 the fp32 vector ALU would spend 2*M flops per streamed
+// weight (M = 16: 42 GFLOP per Phi-1.5 step, ~270 us at the fp32 peak), so
+// the products go to v_mfma_f32_16x16x32_bf16 instead, with no loss of
+// precision:
+//  * codes are small integers (Q8_0: -127..127, Q4_0: c - 8 in -8..7), exact
+//    in bf16;
+//  * x is split into three bf16 parts x = x1 + x2 + x3 (each the top 16 bits
+//    of the remaining fp32 residual; the residuals are exact), which carries
+//    24 significant bits, fp32's own precision, over fp32's exponent range;
+//  * bf16 x bf16 products are exact in fp32 and the MFMA accumulates in fp32;
+//  * the block scale d (fp16, exact in fp32) is applied once per block of 32
+//    weights: acc += d * (sum over the block), as in the M = 1 kernel.
+// One MFMA covers 16 weight rows x one block of 32 weights x 16 rows of X
+// (rows m >= M are zero).  Operand layout of v_mfma_f32_16x16x32_bf16: lane l
+// supplies A[l%16][8*(l/16) .. +7] and B[8*(l/16) .. +7][l%16]; accumulator
+// register i of lane l is D[4*(l/16) + i][l%16].  Here A = X (row m = l%16)
+// and B = w^T (weight row n0 + l%16), so lane l reads 8 consecutive codes of
+// its weight row: Q8_0 bytes 8q..8q+7 of the block (q = l/16), Q4_0 the low
+// (q < 2) or high (q >= 2) nibbles of bytes 8*(q&1)..+7 (byte j holds weights
+// j and j + 16).
+//
+// A block of NW waves owns R groups of 16 weight rows; wave w takes the w-th
+// NW-th of the K blocks and walks it in steps of G = 4 blocks.  Codes do not
+// go straight to registers: in the MFMA layout a wave instruction would touch
+// 16 rows x 32 bytes (16 partly used lines), and such loads ran at a fraction
+// of HBM speed whatever the arithmetic.  Instead each step's codes of the
+// wave's rows (16R rows x 128 bytes for Q8_0, x 64 bytes for Q4_0) are copied
+// into the wave's own LDS slot with direct 16-byte loads (1 KiB contiguous
+// per instruction), double-buffered, and read back per lane (ds_read_b64).
+// The 16-byte pieces of each LDS row are XOR-swizzled with row bits so the
+// 16 lanes of a read hit distinct banks.  The block's scales (all K) are
+// staged once per block.  X goes straight to registers, one step ahead.
+// The NW partial tiles meet in LDS.  Splitting K over blocks instead (to give
+// small-N problems more blocks) would need a cross-block combine; on MI355X a
+// device-scope release fence per block costs ~90 ns, serialized (1024 blocks:
+// ~96 us), so small N gets 16-wave blocks instead.
+#include "common.h"
+#include "device_math.h"
+
+namespace mvlm {
+
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8v;
+
+// top 16 bits of two floats -> one packed bf16 pair (truncation)
+__device__ __forceinline__ uint32_t pack_hi16(float lo_elem, float hi_elem) {
+    return __builtin_amdgcn_perm(__float_as_uint(hi_elem), __float_as_uint(lo_elem), 0x07060302u);
+}
+
+// x[0..7] -> three bf16x8 parts with x = p1 + p2 + p3 (+ |residual| < 2^-24 |x|)
+__device__ __forceinline__ void split3(const float (&x)[8], u32x4& p1, u32x4& p2, u32x4& p3) {
+    float r1[8], r2[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float a = __uint_as_float(__float_as_uint(x[j]) & 0xFFFF0000u);
+        r1[j] = x[j] - a;                                   // exact
+        const float b = __uint_as_float(__float_as_uint(r1[j]) & 0xFFFF0000u);
+        r2[j] = r1[j] - b;                                  // exact
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        p1[j] = pack_hi16(x[2 * j], x[2 * j + 1]);
+        p2[j] = pack_hi16(r1[2 * j], r1[2 * j + 1]);
+        p3[j] = pack_hi16(r2[2 * j], r2[2 * j + 1]);
+    }
+}
+
+// 8 small integers (exact in bf16) from 8 code bytes / nibbles
+template <bool Q4>
+__device__ __forceinline__ u32x4 codes_to_bf16(u32x2 raw, int q) {
+    float v[8];
+    if constexpr (Q4) {
+        const int shift = (q >> 1) * 4;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = (float)((int)((raw[j >> 2] >> (8 * (j & 3) + shift)) & 0xFu) - 8);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = (float)(int8_t)(raw[j >> 2] >> (8 * (j & 3)));
+    }
+    u32x4 out;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out[j] = pack_hi16(v[2 * j], v[2 * j + 1]);
+    return out;
+}
+
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, a), __builtin_bit_cast(bf16x8v, b), c,
+                                                   0, 0, 0);
+}
+
+constexpr int SK_G = 4;          // K blocks per step
+constexpr size_t SKINNY_LDS_MAX = 160 * 1024;
+
+template <bool Q4>
+struct SkinnyLayout {
+    static constexpr int BB = Q4 ? 16 : 32;           // code bytes per block per row
+    static constexpr int CB = SK_G * BB;              // code bytes per row per step (64 / 128)
+    static constexpr int P = CB / 16;                 // 16-byte pieces per row per step
+    static constexpr int RPI = 64 / P;                // rows per direct-load instruction
+    // physical piece of logical piece p in LDS row r
+    __device__ static int piece(int p, int r) { return p ^ (Q4 ? ((r >> 2) & 3) : ((r >> 1) & 7)); }
+};
+
+// LDS bytes of a block: the scales of its rows (all K), then two code slots
+// per wave; the partial tiles of the final combine reuse the slots.
+template <bool Q4, int R, int NW>
+__host__ __device__ constexpr int skinny_slot_bytes() { return 16 * R * SkinnyLayout<Q4>::CB; }
+template <bool Q4, int R, int NW>
+static size_t skinny_lds_bytes(int K) {
+    const size_t scale_region = ((size_t)16 * R * (K / 32) * 2 + 255) / 256 * 256;
+    return scale_region + (size_t)NW * 2 * skinny_slot_bytes<Q4, R, NW>();
+}
+
+template <bool Q4, int R, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(const float* __restrict__ X,
+                                                              const uint8_t* __restrict__ codes,
+                                                              const uint16_t* __restrict__ scales,
+                                                              float* __restrict__ Y, int M, int N, int K,
+                                                              int64_t ld) {
+    using L = SkinnyLayout<Q4>;
+    constexpr int ROWS = 16 * R;
+    constexpr int SLOT = skinny_slot_bytes<Q4, R, NW>();
+    constexpr int NDMA = ROWS / L::RPI;               // direct loads per step
+    static_assert(NDMA <= 63, "direct loads of one step must fit vmcnt");
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15, q = lane >> 4;
+    const int n0 = blockIdx.x * ROWS;
+    const int nb = K >> 5;
+    const int per = (nb + NW - 1) / NW;
+    const int b0 = wave * per, b1 = min(b0 + per, nb);
+    const int steps = b1 > b0 ? (b1 - b0 + SK_G - 1) / SK_G : 0;
+    const int64_t row_bytes = (int64_t)nb * L::BB;
+
+    // scales of rows n0 .. n0+ROWS-1 (contiguous in the scale array) with
+    // 4-byte direct loads (a direct load writes lane i's data at base + 4i
+    // whatever its width, so 2-byte loads would not pack).  Reads are clamped
+    // to the last whole dword of the array (the allocation pads it); rows
+    // past N read stale scales and are never stored.
+    const int scale_bytes = ROWS * nb * 2;
+    const int scale_region = (scale_bytes + 255) / 256 * 256;
+    uint8_t* slots = lds + scale_region + wave * 2 * SLOT;
+    const int64_t s_first = (int64_t)n0 * nb * 2, s_last = (((int64_t)N * nb * 2 - 1) & ~(int64_t)3);
+    const uint8_t* scale_bytes_ptr = reinterpret_cast<const uint8_t*>(scales);
+    for (int piece = wave; piece * 256 < scale_bytes; piece += NW) {
+        const int64_t off = min(s_first + piece * 256 + lane * 4, s_last);
+        __builtin_amdgcn_global_load_lds(scale_bytes_ptr + off, (lds_void*)(lds + piece * 256), 4, 0, 0);
+    }
+
+    // one step's direct loads: this wave's code rows into slot (step & 1)
+    const float* xrow = X + (int64_t)min(l16, M - 1) * K + 8 * q;
+    const int dma_row = lane / L::P, dma_piece = lane % L::P;
+    auto issue_codes = [&](int step, int slot_idx) {
+        const int kb = b0 + step * SK_G;
+        uint8_t* slot = slots + slot_idx * SLOT;
+#pragma unroll
+        for (int t = 0; t < NDMA; ++t) {
+            const int r = t * L::RPI + dma_row;
+            const int64_t row = min(n0 + r, N - 1);
+            const int64_t off = min((int64_t)kb * L::BB + 16 * L::piece(dma_piece, r), row_bytes - 16);
+            __builtin_amdgcn_global_load_lds(codes + row * ld + off, (lds_void*)(slot + t * 1024), 16, 0, 0);
+        }
+    };
+    // X of one step into registers
+    auto load_x = [&](int step, u32x4 (&xr)[SK_G][2]) {
+        const int kb = b0 + step * SK_G;
+#pragma unroll
+        for (int g = 0; g < SK_G; ++g) {
+            const int bb = min(kb + g, nb - 1);
+            xr[g][0] = asm_global_load_b128(xrow + 32 * bb);
+            xr[g][1] = asm_global_load_b128(xrow + 32 * bb + 4);
+        }
+    };
+
+    const bool xrow_live = l16 < M;                   // this lane's X row (A row)
+    f32x4 acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (steps > 0) issue_codes(0, 0);
+    asm_wait_vmcnt<0>();
+    __syncthreads();                                  // the staged scales of every wave
+
+    // LDS reads go through inline asm (the compiler would otherwise wait for
+    // every in-flight direct load, including the next step's, before them)
+    const uint32_t lds_base = lds_offset(lds);
+    auto compute = [&](int step, const u32x4 (&xr)[SK_G][2]) {
+        const int kb = b0 + step * SK_G;
+        const uint32_t slot = lds_offset(slots + (step & 1) * SLOT);
+        u32x2 raw[SK_G][R];
+        uint32_t dh[SK_G][R];
+#pragma unroll
+        for (int g = 0; g < SK_G; ++g) {
+            const int lpiece = Q4 ? g : 2 * g + (q >> 1);
+            const int bb = min(kb + g, b1 - 1);
+#pragma unroll
+            for (int rr = 0; rr < R; ++rr) {
+                const int r = 16 * rr + l16;
+                raw[g][rr] = asm_lds_read_b64(slot + r * L::CB + 16 * L::piece(lpiece, r) + 8 * (q & 1));
+                dh[g][rr] = asm_lds_read_u16(lds_base + 2 * (r * nb + bb));
+            }
+        }
+        asm_wait_lgkmcnt<0>();
+#pragma unroll
+        for (int g = 0; g < SK_G; ++g)
+#pragma unroll
+            for (int rr = 0; rr < R; ++rr) {
+                asm_pin(raw[g][rr]);
+                asm_pin(dh[g][rr]);
+            }
+#pragma unroll
+        for (int g = 0; g < SK_G; ++g) {
+            if (kb + g >= b1) continue;               // uniform over the wave
+            float x[8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                x[j] = xrow_live ? __uint_as_float(xr[g][0][j]) : 0.0f;
+                x[4 + j] = xrow_live ? __uint_as_float(xr[g][1][j]) : 0.0f;
+            }
+            u32x4 p1, p2, p3;
+            split3(x, p1, p2, p3);
+#pragma unroll
+            for (int rr = 0; rr < R; ++rr) {
+                const u32x4 w = codes_to_bf16<Q4>(raw[g][rr], q);
+                f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+                c = mfma16(p1, w, c);
+                c = mfma16(p2, w, c);
+                c = mfma16(p3, w, c);
+                const float d = f16_bits_to_f32((uint16_t)dh[g][rr]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[rr][i] = __builtin_fmaf(d, c[i], acc[rr][i]);
+            }
+        }
+    };
+
+    // Per step: X loads (L2-resident, consumed in the same iteration), then the
+    // next step's codes (the last step re-reads its own codes into the idle
+    // slot, which keeps the count uniform); waiting until only those remain in
+    // flight covers this step's X and codes.  X also goes through untracked
+    // loads, so the compiler adds no waits of its own in the loop.
+    for (int step = 0; step < steps; ++step) {
+        u32x4 xr[SK_G][2];
+        load_x(step, xr);
+        issue_codes(step + 1 < steps ? step + 1 : step, (step + 1) & 1);
+        asm_wait_vmcnt<NDMA>();
+#pragma unroll
+        for (int g = 0; g < SK_G; ++g) {
+            asm_pin(xr[g][0]);
+            asm_pin(xr[g][1]);
+        }
+        compute(step, xr);
+    }
+
+    // combine the NW partial tiles (reusing the code slots)
+    __syncthreads();
+    f32x4* part = reinterpret_cast<f32x4*>(lds + scale_region);
+#pragma unroll
+    for (int r = 0; r < R; ++r) part[(wave * R + r) * 64 + lane] = acc[r];
+    __syncthreads();
+    if (wave < R) {                                   // wave r sums row group r
+        const int r = wave;
+        f32x4 sum = part[r * 64 + lane];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            const f32x4 t = part[(w * R + r) * 64 + lane];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sum[i] += t[i];
+        }
+        const int n = n0 + 16 * r + l16;
+        if (n < N) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = 4 * q + i;
+                if (m < M) Y[(int64_t)m * N + n] = sum[i];
+            }
+        }
+    }
+}
+
+template <bool Q4, int R, int NW>
+static hipError_t launch_skinny(hipStream_t s, const float* X, const mvlm_weight* W, float* Y, int M, int N, int K) {
+    auto kernel = gemm_skinny_kernel<Q4, R, NW>;
+    const size_t lds = skinny_lds_bytes<Q4, R, NW>(K);
+    static bool attr_set = false;
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)SKINNY_LDS_MAX);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    if (lds > SKINNY_LDS_MAX) return hipErrorInvalidValue;
+    const unsigned blocks = (unsigned)((N + 16 * R - 1) / (16 * R));
+    launch_kernel(kernel, dim3(blocks), dim3(64 * NW), (uint32_t)lds, s, X, (const uint8_t*)W->data,
+                  (const uint16_t*)W->scales, Y, M, N, K, (int64_t)W->ld);
+    return hipGetLastError();
+}
+
+// Two row groups per block when that still gives every CU a block; fewer
+// row groups than CUs get 16-wave blocks (more loads in flight per block).
+template <bool Q4>
+static hipError_t launch_skinny_shape(hipStream_t s, const float* X, const mvlm_weight* W, float* Y, int M, int N,
+                                      int K, int num_cus) {
+    const int groups = (N + 15) / 16;
+    if (groups >= 2 * num_cus) return launch_skinny<Q4, 2, 8>(s, X, W, Y, M, N, K);
+    if (groups >= num_cus) return launch_skinny<Q4, 1, 8>(s, X, W, Y, M, N, K);
+    return launch_skinny<Q4, 1, 16>(s, X, W, Y, M, N, K);
+}
+
+hipError_t launch_gemm_skinny(hipStream_t s, const float* X, const mvlm_weight* W, float* Y, int M, int N, int K,
+                              int num_cus) {
+    if (M < 1 || M > 16 || K % 32 != 0 || !is_quant(W->dtype)) return hipErrorInvalidValue;
+    if (num_cus <= 0) num_cus = 256;
+    if (W->dtype == MVLM_Q4_0) return launch_skinny_shape<true>(s, X, W, Y, M, N, K, num_cus);
+    return launch_skinny_shape<false>(s, X, W, Y, M, N, K, num_cus);
+}
+
+}  // namespace mvlm

@@ -112,8 +112,6 @@ __device__ __forceinline__ float chunk_dot(Q4Fmt, u32x4 q, uint16_t dh, const XR
 
 // ---- LDS staging -------------------------------------------------------------
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 // A lane's x values for one chunk are XB = WPL * sizeof(XT) consecutive bytes
 // (8 .. 128).  Read from LDS as 16-byte slots, lane l reads slot SL*l + i in
 // its i-th read; 16 lanes share one LDS cycle, so with SL > 1 lanes l and
@@ -142,13 +140,6 @@ __device__ __forceinline__ void stage_to_lds(uint8_t* dst, const uint8_t* __rest
     }
 }
 
-// s_waitcnt with vmcnt = n and expcnt / lgkmcnt unconstrained (gfx9 encoding)
-template <int n>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(n >= 0 && n < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 // ---- the kernel ------------------------------------------------------------
 
 // One problem of a grouped launch.  Chunk c of a row covers bytes
@@ -170,7 +161,10 @@ struct StreamProblem {
 };
 
 constexpr int MAX_GROUP = 8;
-constexpr int NWAVE = 8;           // waves per block
+#ifndef MVLM_STREAM_WAVES
+#define MVLM_STREAM_WAVES 8
+#endif
+constexpr int NWAVE = MVLM_STREAM_WAVES;   // waves per block
 
 struct StreamGroup {
     StreamProblem p[MAX_GROUP];
@@ -196,7 +190,7 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
     constexpr int WPL = F::WPL;
     constexpr int XB = WPL * (int)sizeof(XT);        // x bytes per lane per chunk
     constexpr int SL = XB >= 16 ? XB / 16 : 1;       // 16-byte LDS slots per lane per chunk
-    const int N = P.N, K = P.K, nb = K >> 5;
+    const int K = P.K, nb = K >> 5;
     const int wsub = wave % SPLIT;
     const int row0 = rb0 + (wave / SPLIT) * R;
     const bool active = row0 < rb1;
@@ -302,7 +296,9 @@ __global__ __launch_bounds__(64 * NWAVE, F::MIN_WAVES) void gemv_stream_kernel(c
     for (int i = 1; i < MAX_GROUP; ++i)
         if (i < g.count && (int)blockIdx.x >= g.p[i].block_begin) pi = i;
     const StreamProblem& P = g.p[pi];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // the wave index is uniform: keep it in a scalar register so the staging
+    // loops and row offsets are scalar code
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int N = P.N, K = P.K, nb = K >> 5;
     const int rb0 = ((int)blockIdx.x - P.block_begin) * P.rows_per_block;
     const int rb1 = min(rb0 + P.rows_per_block, N);

@@ -188,7 +188,7 @@ hipError_t enqueue_op(hipStream_t s, const Op& op) {
         case OP_GEMV_QUANT:
             if (op.M == 1 && stream_supported(op.w))
                 return launch_gemv_stream(s, op.a, MVLM_F32, op.w, op.c, MVLM_F32, op.num_cus);
-            return launch_gemv_quant(s, (const float*)op.a, op.w, (float*)op.c, op.M, op.N, op.K);
+            return launch_gemm_skinny(s, (const float*)op.a, op.w, (float*)op.c, op.M, op.N, op.K, op.num_cus);
     }
     return hipErrorInvalidValue;
 }

@@ -216,6 +216,28 @@ def test_quant_skinny_gemm(dev, orc, qt, M):
     assert ok, worst
 
 
+@pytest.mark.parametrize("qt", [Q8, Q4])
+@pytest.mark.parametrize("M,N,K,xscale", [(4, 33, 32, 1.0), (16, 17, 96, 1.0), (3, 130, 8192, 1.0),
+                                          (16, 6144, 2048, 1.0), (7, 300, 2048, 3.0e4), (9, 64, 1024, 1.0e-6),
+                                          (2, 51, 23 * 32, 1.0), (5, 8200, 96, 1.0), (16, 16400, 64, 1.0)])
+def test_quant_skinny_shapes(dev, orc, qt, M, N, K, xscale):
+    # ragged N (not a multiple of the 16-row MFMA tile), fewer K blocks than
+    # waves, long rows, x far from unit scale (the bf16 three-way split of x
+    # must keep fp32 precision over fp32's range), and N large enough for the
+    # blocks with 2 and 4 row groups (ragged in the last block)
+    X = (orc.normal_f32(M * K, 171) * np.float32(xscale)).astype(np.float32)
+    blocks = make_quant(orc, qt, N, K, 172)
+    kind = "q8_0" if qt == Q8 else "q4_0"
+    ref = orc.gemm_nk(kind, X, blocks, M, N, K)
+    deq = (orc.dequant_q8_0 if qt == Q8 else orc.dequant_q4_0)(blocks).astype(np.float64).reshape(N, K)
+    _, S = orc.gemm_f64(X.astype(np.float64).reshape(M, K), deq, M, N, K)
+    W = dev.pack(blocks, qt, N, K)
+    dX, dY = dev.upload(X), dev.alloc(M * N * 4)
+    dev.gemm_quant(dX, W, dY, M, N, K)
+    ok, worst = within(dY.download(np.float32).reshape(M, N), ref, S, 1e-5)
+    assert ok, worst
+
+
 def test_weight_random_matches_oracle_generator(dev, orc):
     N, K, seed = 64, 256, 0x1234
     for qt in (Q8, Q4):
