@@ -74,14 +74,9 @@ def profile_plan(plan, reps=5):
 # workloads
 # ---------------------------------------------------------------------------
 
-def decode_step(dev, m, qt, M, steps, warmup, graph=True, grouped=True):
-    """One Phi-1.5 decode step over quantized weights, M rows of activations.
-
-    Phi-1.5 blocks are parallel (attention and MLP read the same normalised
-    input), so per layer QKV and fc1 are independent of each other, and so are
-    dense (on the attention output) and fc2 (on the GELU output).  grouped=True
-    issues each independent pair as one grouped launch (2 launches per layer +
-    the LM head = 49); grouped=False issues the 97 GEMVs one launch each."""
+def build_decode_plan(dev, m, qt, M, grouped=True):
+    """The plan of one Phi-1.5 decode step over quantized weights, M rows of
+    activations (see decode_step).  Returns (plan, weights, grouped)."""
     qdt = m.Q8_0 if qt == "q8_0" else m.Q4_0
     weights = [dev.random_weight(qdt, N, K, SEED ^ (0x100 + i), 0.02) for i, (_, N, K) in enumerate(PHI_STEP)]
     ln = dev.fill_normal(dev.alloc(M * 2048 * 4), m.F32, M * 2048, SEED ^ 0x11, 1.0)     # block input
@@ -100,6 +95,18 @@ def decode_step(dev, m, qt, M, steps, warmup, graph=True, grouped=True):
     else:
         for W, (name, N, K) in zip(weights, PHI_STEP):
             plan.add_gemv(x_of[name], m.F32, W, ys[name], m.F32, M)
+    return plan, weights, grouped
+
+
+def decode_step(dev, m, qt, M, steps, warmup, graph=True, grouped=True):
+    """One Phi-1.5 decode step over quantized weights, M rows of activations.
+
+    Phi-1.5 blocks are parallel (attention and MLP read the same normalised
+    input), so per layer QKV and fc1 are independent of each other, and so are
+    dense (on the attention output) and fc2 (on the GELU output).  grouped=True
+    issues each independent pair as one grouped launch (2 launches per layer +
+    the LM head = 49); grouped=False issues the 97 GEMVs one launch each."""
+    plan, weights, grouped = build_decode_plan(dev, m, qt, M, grouped)
     per_op = profile_plan(plan)
     if graph:
         plan.use_graph(True)
@@ -209,6 +216,89 @@ def cpu_baseline(seconds=10.0):
 
 
 # ---------------------------------------------------------------------------
+# HBM traffic of the headline step from rocprofv3 counters
+# ---------------------------------------------------------------------------
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_phi15_decode_q8_0.json")
+COPY_BYTES = 256 << 20
+
+
+def pmc_probe(steps=3):
+    """Workload for the counter runs: `steps` eager headline steps (49 kernels
+    each), then a plain device-to-device copy of COPY_BYTES (the calibration:
+    what FETCH_SIZE / WRITE_SIZE read for a kernel of known traffic)."""
+    import mvlm_amd as m
+    import torch
+    dev = m.Device(0)
+    plan, weights, _ = build_decode_plan(dev, m, "q8_0", 1, True)
+    plan.run(1)
+    dev.sync()
+    plan.run(steps)
+    dev.sync()
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    plan.destroy()
+    for W in weights:
+        W.free()
+    dev.close()
+    print("pmc probe done", flush=True)
+
+
+def _counter_rows(d):
+    import csv
+    import glob
+    f = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    if not f:
+        raise SystemExit(f"no counter_collection.csv under {d}")
+    per = {}
+    for r in csv.DictReader(open(f[0])):
+        key = int(r["Dispatch_Id"])
+        e = per.setdefault(key, {"name": r["Kernel_Name"], "grid": int(r.get("Grid_Size", 0) or 0), "value": 0.0})
+        e["value"] += float(r["Counter_Value"])
+    return [per[k] for k in sorted(per)]
+
+
+def pmc_summarize(fetch_dir, write_dir, out=TRAFFIC_FILE):
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the last headline step and
+    of the calibration copy -> HBM bytes per step, scaled by the copy's
+    measured/true ratio."""
+    res = {}
+    for counter, d in (("fetch", fetch_dir), ("write", write_dir)):
+        rows = _counter_rows(d)
+        gemv = [r for r in rows if "gemv_stream_kernel" in r["name"]]
+        copy = [r for r in rows if "copy" in r["name"].lower() or "elementwise" in r["name"].lower()]
+        step = gemv[-49:]
+        raw = sum(r["value"] for r in step) * 1024.0
+        cal = (min(r["value"] for r in copy[-3:]) * 1024.0) / COPY_BYTES if copy else 1.0
+        res[counter] = {"raw_bytes_per_step": raw, "copy_factor": cal, "bytes_per_step": raw / cal,
+                        "copy_kernel": copy[-1]["name"][:80] if copy else None, "launches": len(step)}
+    alg = float(sum(gemv_bytes("q8_0", N, K, 1) for _, N, K in PHI_STEP))
+    total = res["fetch"]["bytes_per_step"] + res["write"]["bytes_per_step"]
+    summary = {"workload": "phi15_decode_q8_0", "algorithmic_bytes_per_step": alg,
+               "hbm_bytes_per_step": total, "ratio_to_algorithmic": total / alg, "fetch": res["fetch"],
+               "write": res["write"],
+               "command": "cd /tmp && export TMPDIR=/tmp && rocprofv3 --pmc FETCH_SIZE -d $R/gpurun_out/pmc_fetch "
+                          "-o run --output-format csv -- python3 $R/bench.py --pmc-probe; same with WRITE_SIZE "
+                          "into pmc_write; python3 $R/bench.py --pmc-summarize gpurun_out/pmc_fetch "
+                          "gpurun_out/pmc_write   (R = repository root)"}
+    with open(out, "w") as fh:
+        json.dump(summary, fh, indent=1)
+    print(json.dumps(summary, indent=1))
+
+
+def measured_traffic():
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            return float(json.load(fh)["hbm_bytes_per_step"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+# ---------------------------------------------------------------------------
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
@@ -219,7 +309,16 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="enqueue plans eagerly instead of replaying HIP graphs")
+    ap.add_argument("--pmc-probe", action="store_true", help="workload for rocprofv3 --pmc traffic runs")
+    ap.add_argument("--pmc-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="turn the two counter runs into " + os.path.relpath(TRAFFIC_FILE, ROOT))
     args = ap.parse_args()
+    if args.pmc_summarize:
+        pmc_summarize(*args.pmc_summarize)
+        return
+    if args.pmc_probe:
+        pmc_probe()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the decode GEMV would shard "
               "along N, see DESIGN.md); run with --gpus 1", file=sys.stderr)
@@ -288,7 +387,9 @@ def main():
                                "Phi-1.5's parallel block); LM head alone",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(head["kernel_gbs"], 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(head["kernel_frac"], 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(head["kernel_frac"], 4), "traffic": measured_traffic(),
+                     "traffic_note": "HBM bytes per step (49 launches) from rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                                     "scaled by a 256 MiB device copy; " + os.path.relpath(TRAFFIC_FILE, ROOT),
                      "kernel": "gemv_stream_kernel<Q8Fmt>",
                      "timing": f"algorithmic bytes of one step / sum of the {head['launches']} kernel "
                                "execution times, each from HIP start/stop events on the launch's own dispatch "
