@@ -118,6 +118,18 @@ __device__ __forceinline__ uint32_t asm_lds_read_u16(uint32_t addr) {
     asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
     return v;
 }
+// A direct global->LDS 16-byte load the compiler does not track: lane i's 16
+// bytes from gaddr land at LDS byte lds_base + 16 * i (lds_base wave-uniform).
+// The compiler puts a vmcnt(0) in front of every tracked direct load that may
+// overwrite LDS written by an earlier one, which caps a multi-stage ring at
+// one stage in flight; with this form the kernel's own waits order the ring.
+__device__ __forceinline__ void asm_global_load_lds_b128(const void* gaddr, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(gaddr), "s"(lds_base)
+                 : "memory", "m0");
+}
+
 // A 16-byte global load the compiler does not track (wait with
 // asm_wait_vmcnt, then asm_pin the result).
 __device__ __forceinline__ u32x4 asm_global_load_b128(const void* p) {

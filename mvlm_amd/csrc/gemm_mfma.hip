@@ -75,7 +75,7 @@ __device__ __forceinline__ void stage_direct(const uint16_t* __restrict__ base, 
         const int g = wave + NW * t;
         const int r = min(r0 + 8 * g + (lane >> 3), rmax);
         const uint16_t* src = base + (int64_t)r * ld + k0 + ls * 8;
-        __builtin_amdgcn_global_load_lds(src, (lds_void*)(lds + 8 * g * ROWH), 16, 0, 0);
+        asm_global_load_lds_b128(src, __builtin_amdgcn_readfirstlane(lds_offset(lds + 8 * g * ROWH)));
     }
 }
 
@@ -145,22 +145,32 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(const GemmArg
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    // fragment reads of k-step ks of the stage held in ring slot `slot`
+    // Fragment reads of k-step ks of the stage held in ring slot `slot_idx`.
+    // They are inline-asm LDS reads with explicit waits (device_math.h): the
+    // compiler's own waits would put vmcnt(0) before every read (the ring is
+    // filled by direct loads) and merge the loop-carried reads into
+    // lgkmcnt(0).  Row r of a fragment is lane&31 plus a multiple of 32, so its
+    // swizzle (r >> 1) & 7 is the lane's; byte offsets: row * 128 + slot * 16.
     struct Frags { u32x4 a[TM]; u32x4 b[TN]; };
+    const uint32_t lds0 = lds_offset(smem);
+    const uint32_t a_lane = (uint32_t)((wm * WM + (lane & 31)) * ROWH * 2);
+    const uint32_t b_lane = (uint32_t)((BM + wn * WN + (lane & 31)) * ROWH * 2);
+    const int swz = (lane >> 1) & 7, half = lane >> 5;
     auto load_frags = [&](int slot_idx, int ks, Frags& f) {
-        const uint16_t* As = smem + slot_idx * SLOT;
-        const uint16_t* Bs = As + BM * ROWH;
-        const int s = 2 * ks + (lane >> 5);
+        const uint32_t base = lds0 + (uint32_t)(slot_idx * SLOT * 2) + (uint32_t)((((2 * ks + half) ^ swz)) << 4);
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            const int r = wm * WM + i * 32 + (lane & 31);
-            f.a[i] = *reinterpret_cast<const u32x4*>(As + r * ROWH + ((s ^ ((r >> 1) & 7)) << 3));
-        }
+        for (int i = 0; i < TM; ++i) f.a[i] = asm_lds_read_b128(base + a_lane + i * 32 * ROWH * 2);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int r = wn * WN + j * 32 + (lane & 31);
-            f.b[j] = *reinterpret_cast<const u32x4*>(Bs + r * ROWH + ((s ^ ((r >> 1) & 7)) << 3));
-        }
+        for (int j = 0; j < TN; ++j) f.b[j] = asm_lds_read_b128(base + b_lane + j * 32 * ROWH * 2);
+    };
+    // wait until at most `newer` LDS reads are pending, then tie f to the wait
+    auto ready = [&](Frags& f, bool newer) {
+        if (newer) asm_wait_lgkmcnt<TM + TN>();
+        else asm_wait_lgkmcnt<0>();
+#pragma unroll
+        for (int i = 0; i < TM; ++i) asm_pin(f.a[i]);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) asm_pin(f.b[j]);
     };
     auto mma = [&](const Frags& f) {
 #pragma unroll
@@ -173,13 +183,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(const GemmArg
     // flight (vmcnt counts them in issue order).
     auto wait_stage = [&](int s, int later) {
         const int later_direct = later - ((later > 0 && s + later == nk - 1 && (tail_a || tail_b)) ? 1 : 0);
-        if (later_direct >= 2) wait_vmcnt<(2 * LA <= 63) ? 2 * LA : LA>();   // LA: conservative
-        else if (later_direct == 1) wait_vmcnt<LA>();
-        else wait_vmcnt<0>();
+        if (later_direct >= 2) asm_wait_vmcnt<(2 * LA <= 63) ? 2 * LA : LA>();   // LA: conservative
+        else if (later_direct == 1) asm_wait_vmcnt<LA>();
+        else asm_wait_vmcnt<0>();
         // A bare s_barrier, not __syncthreads(): the latter's release fence
-        // would wait for every in-flight stage (vmcnt(0)).  The guarded stage
-        // writes LDS with ds_write, so LDS traffic is drained first.
-        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt, expcnt unconstrained
+        // would wait for every in-flight stage (vmcnt(0)).  LDS traffic (this
+        // wave's last fragment reads of the slot about to be refilled, and the
+        // guarded stage's ds_writes) is drained first.
+        asm_wait_lgkmcnt<0>();
         __builtin_amdgcn_s_barrier();
     };
 
@@ -213,25 +224,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(const GemmArg
                 if (kt + STAGES < nk) issue(kt + STAGES);
                 load_frags((kt + 1) % STAGES, 0, nxt);
             }
-            __builtin_amdgcn_sched_barrier(0);
             // LDS reads complete in order: with the TM+TN reads of the next set
             // issued last, lgkmcnt(TM+TN) means this set has landed.  (At the
-            // last k-step of the last stage nothing newer is pending and the
-            // same count still holds.)
-            if (ks < BK / 16 - 1 || kt + 1 < nk)
-                __builtin_amdgcn_s_waitcnt(0xC07F | ((TM + TN) << 8));   // lgkmcnt(TM+TN)
-            else
-                __builtin_amdgcn_s_waitcnt(0xC07F);                      // lgkmcnt(0)
+            // last k-step of the last stage nothing newer is pending.)
+            ready(f[ks & 1], ks < BK / 16 - 1 || kt + 1 < nk);
             mma(f[ks & 1]);
-            __builtin_amdgcn_sched_barrier(0);
         }
-        // The next stage's first fragments (read during the last k-step) have
-        // had a whole k-step of MFMAs to land.  Waiting for them here leaves no
-        // LDS read pending across the loop back-edge; otherwise the compiler's
-        // wait insertion merges the entry and back-edge states and puts a full
-        // lgkmcnt(0) in front of the first MFMA of every stage, after the next
-        // k-step's reads have been issued.
-        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
     }
 
     const int64_t c_off = (int64_t)blockIdx.z * p.sC;
