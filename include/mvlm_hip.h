@@ -40,7 +40,9 @@ enum mvlm_status {
     MVLM_ERR_OUT_OF_MEMORY = -3, /* device or host allocation failed        */
     MVLM_ERR_HIP = -4,           /* a HIP runtime call failed               */
     MVLM_ERR_UNSUPPORTED = -5,   /* valid request this build does not serve */
-    MVLM_ERR_BUFFER_TOO_SMALL = -6
+    MVLM_ERR_BUFFER_TOO_SMALL = -6,
+    MVLM_ERR_NOT_FOUND = -7,     /* no such tensor / metadata key            */
+    MVLM_ERR_FORMAT = -8         /* malformed or truncated file              */
 };
 
 /* ---- element types (ggml type ids, src/models/gguf_loader.h:12-31) ----- */

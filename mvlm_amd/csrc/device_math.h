@@ -123,12 +123,18 @@ __device__ __forceinline__ uint32_t asm_lds_read_u16(uint32_t addr) {
 // The compiler puts a vmcnt(0) in front of every tracked direct load that may
 // overwrite LDS written by an earlier one, which caps a multi-stage ring at
 // one stage in flight; with this form the kernel's own waits order the ring.
+// M0 is reserved to the compiler, which sets it before each of its own uses
+// (direct loads, GWS, messages; LDS reads/writes do not use it on gfx950), so
+// the clobber below documents the write rather than being needed.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void asm_global_load_lds_b128(const void* gaddr, uint32_t lds_base) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                  :
                  : "v"(gaddr), "s"(lds_base)
                  : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // A 16-byte global load the compiler does not track (wait with
 // asm_wait_vmcnt, then asm_pin the result).

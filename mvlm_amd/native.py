@@ -22,6 +22,7 @@ DTYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16", Q8_0: "q8_0", Q4_0: "q4_0"}
 
 OK = 0
 ERR_INVALID_ARG, ERR_NO_DEVICE, ERR_OUT_OF_MEMORY, ERR_HIP, ERR_UNSUPPORTED, ERR_BUFFER_TOO_SMALL = -1, -2, -3, -4, -5, -6
+ERR_NOT_FOUND, ERR_FORMAT = -7, -8
 
 
 class MvlmError(RuntimeError):
@@ -36,6 +37,16 @@ class DeviceInfo(ctypes.Structure):
                 ("memory_clock_mhz", c_int), ("memory_bus_width_bits", c_int), ("wavefront_size", c_int),
                 ("global_mem_size", c_uint64), ("local_mem_size", c_uint64), ("l2_cache_size", c_uint64),
                 ("peak_hbm_gbs", c_double), ("peak_fp16_tflops", c_double)]
+
+
+class GgufInfo(ctypes.Structure):
+    _fields_ = [("version", ctypes.c_uint32), ("tensor_count", c_uint64), ("metadata_kv_count", c_uint64),
+                ("alignment", c_uint64), ("data_offset", c_uint64), ("file_size", c_uint64)]
+
+
+class GgufTensor(ctypes.Structure):
+    _fields_ = [("name", c_void_p), ("name_len", c_uint64), ("n_dims", ctypes.c_uint32),
+                ("dims", c_uint64 * 4), ("type", ctypes.c_uint32), ("offset", c_uint64), ("bytes", c_uint64)]
 
 
 class GemvDesc(ctypes.Structure):
@@ -102,6 +113,18 @@ _SIGNATURES = {
     "mvlm_plan_profile": (c_int, [_P, POINTER(c_float), c_int]),
     "mvlm_marker_record": (c_int, [_P, _PP]),
     "mvlm_marker_elapsed_ms": (c_int, [_P, _P, POINTER(c_float)]),
+    "mvlm_gguf_open": (c_int, [c_char_p, _PP]),
+    "mvlm_gguf_close": (c_int, [_P]),
+    "mvlm_gguf_get_info": (c_int, [_P, POINTER(GgufInfo)]),
+    "mvlm_gguf_tensor_info": (c_int, [_P, c_uint64, POINTER(GgufTensor)]),
+    "mvlm_gguf_find_tensor": (c_int, [_P, c_char_p, POINTER(c_uint64)]),
+    "mvlm_gguf_tensor_data": (c_int, [_P, c_uint64, _PP]),
+    "mvlm_gguf_get_u32": (c_int, [_P, c_char_p, POINTER(ctypes.c_uint32)]),
+    "mvlm_gguf_get_string": (c_int, [_P, c_char_p, _PP, POINTER(c_uint64)]),
+    "mvlm_gguf_get_array": (c_int, [_P, c_char_p, POINTER(ctypes.c_uint32), POINTER(c_uint64), _PP]),
+    "mvlm_gguf_get_array_string": (c_int, [_P, c_char_p, c_uint64, _PP, POINTER(c_uint64)]),
+    "mvlm_ggml_type_size": (c_int, [ctypes.c_uint32, POINTER(c_uint64), POINTER(ctypes.c_uint32)]),
+    "mvlm_weight_from_gguf": (c_int, [_P, _P, c_uint64, _PP]),
 }
 
 _lib = None
@@ -241,6 +264,86 @@ class Weight:
             pass
 
 
+class Gguf:
+    """A memory-mapped GGUF file (include/mvlm_gguf.h); parsing runs in the C
+    library, tensors and strings are read through the mapping."""
+
+    _NP = {0: np.uint8, 1: np.int8, 2: np.uint16, 3: np.int16, 4: np.uint32, 5: np.int32, 6: np.float32,
+           7: np.uint8, 10: np.uint64, 11: np.int64, 12: np.float64}
+
+    def __init__(self, path: str):
+        h = c_void_p()
+        _call("mvlm_gguf_open", os.fsencode(path), byref(h))
+        self.handle = h
+
+    def info(self) -> GgufInfo:
+        out = GgufInfo()
+        _call("mvlm_gguf_get_info", self.handle, byref(out))
+        return out
+
+    def tensor(self, index: int) -> dict:
+        t = GgufTensor()
+        _call("mvlm_gguf_tensor_info", self.handle, index, byref(t))
+        return {"name": ctypes.string_at(t.name, t.name_len).decode(), "n_dims": t.n_dims,
+                "dims": list(t.dims), "type": t.type, "offset": t.offset, "bytes": t.bytes}
+
+    def find(self, name: str) -> int:
+        i = c_uint64()
+        _call("mvlm_gguf_find_tensor", self.handle, name.encode(), byref(i))
+        return i.value
+
+    def data(self, index: int) -> bytes:
+        p = c_void_p()
+        _call("mvlm_gguf_tensor_data", self.handle, index, byref(p))
+        return ctypes.string_at(p, self.tensor(index)["bytes"])
+
+    def get_u32(self, key: str) -> int:
+        v = ctypes.c_uint32()
+        _call("mvlm_gguf_get_u32", self.handle, key.encode(), byref(v))
+        return v.value
+
+    def get_string(self, key: str) -> str:
+        p, n = c_void_p(), c_uint64()
+        _call("mvlm_gguf_get_string", self.handle, key.encode(), byref(p), byref(n))
+        return ctypes.string_at(p, n.value).decode()
+
+    def get_array(self, key: str):
+        et, n, p = ctypes.c_uint32(), c_uint64(), c_void_p()
+        _call("mvlm_gguf_get_array", self.handle, key.encode(), byref(et), byref(n), byref(p))
+        if et.value == 8:
+            out = []
+            for i in range(n.value):
+                s, ln = c_void_p(), c_uint64()
+                _call("mvlm_gguf_get_array_string", self.handle, key.encode(), i, byref(s), byref(ln))
+                out.append(ctypes.string_at(s, ln.value).decode())
+            return out
+        dt = np.dtype(self._NP[et.value])
+        return np.frombuffer(ctypes.string_at(p, n.value * dt.itemsize), dtype=dt).copy()
+
+    def close(self) -> None:
+        if self.handle:
+            _call("mvlm_gguf_close", self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def ggml_type_size(t: int):
+    b, e = c_uint64(), ctypes.c_uint32()
+    _call("mvlm_ggml_type_size", t, byref(b), byref(e))
+    return b.value, e.value
+
+
 def _ev(want: bool):
     return (c_void_p(), True) if want else (None, False)
 
@@ -360,6 +463,11 @@ class Device:
     def pack_device(self, src: Buffer, dtype: int, N: int, K: int, layout: int = LAYOUT_NK) -> Weight:
         h = c_void_p()
         _call("mvlm_weight_pack_device", self.handle, src.handle, dtype, layout, N, K, byref(h))
+        return Weight(self, h)
+
+    def weight_from_gguf(self, g: "Gguf", index: int) -> Weight:
+        h = c_void_p()
+        _call("mvlm_weight_from_gguf", self.handle, g.handle, index, byref(h))
         return Weight(self, h)
 
     def random_weight(self, dtype: int, N: int, K: int, seed: int, wstd: float = 0.02) -> Weight:

@@ -7,20 +7,24 @@ import re
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "mvlm_hip.h")
+INCLUDE = os.path.join(ROOT, "include")
 
 
 def declared_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(mvlm_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in sorted(os.listdir(INCLUDE)):
+        if h.endswith(".h"):
+            text = re.sub(r"/\*.*?\*/", "", open(os.path.join(INCLUDE, h)).read(), flags=re.S)
+            names.update(re.findall(r"\b(mvlm_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_declares_the_boundary():
     names = declared_functions()
     for must in ["mvlm_gemm_naive", "mvlm_gemm_tiled", "mvlm_gemm_packed", "mvlm_gemv",
                  "mvlm_gemv_q8_0", "mvlm_gemv_q4_0", "mvlm_gemm_q8_0", "mvlm_gemm_q4_0",
-                 "mvlm_gemm_batched", "mvlm_weight_pack", "mvlm_pool_init", "mvlm_device_create"]:
+                 "mvlm_gemm_batched", "mvlm_weight_pack", "mvlm_pool_init", "mvlm_device_create",
+                 "mvlm_gguf_open", "mvlm_gguf_find_tensor", "mvlm_weight_from_gguf"]:
         assert must in names
 
 
