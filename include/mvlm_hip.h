@@ -153,6 +153,38 @@ int mvlm_gemm_packed(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, const 
 int mvlm_gemv(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W,
               mvlm_buffer* y, int y_dtype, int N, int K, mvlm_event** ev);
 
+/* ---- fused epilogues ----------------------------------------------------------
+ * out = act(acc + bias[n]) * mul[m][n] + residual[m][n], applied to the fp32
+ * accumulator before the output is rounded to its dtype, so the bias add,
+ * activation, gate product and residual add of a transformer block cost no
+ * extra pass over HBM.  Replaces the separate kernels the reference runs
+ * after its projections: bias adds (vision.cl:178-186, 433-436), gelu
+ * (activations.cl:66-118), silu / silu_gate_multiply (activations.cl:22-60,
+ * 204-255) and vector_add for residuals (activations.cl:259-290).
+ * MVLM_ACT_GELU_TANH is 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), the
+ * formula of activations.cl:68 (the kernel there evaluates the tanh with the
+ * sign flipped, activations.cl:96-116, which this build does not reproduce).
+ * bias ([N]), mul and residual ([M][N], row stride N) are optional, have the
+ * output's dtype, and may alias the output. */
+enum mvlm_activation {
+    MVLM_ACT_NONE = 0,
+    MVLM_ACT_GELU_TANH = 1,
+    MVLM_ACT_SILU = 2          /* x / (1 + exp(-x)) */
+};
+typedef struct mvlm_epilogue {
+    const mvlm_buffer* bias;
+    int activation;
+    const mvlm_buffer* mul;
+    const mvlm_buffer* residual;
+} mvlm_epilogue;
+/* mvlm_gemm_packed / mvlm_gemv with an epilogue (NULL = none).  For
+ * quantized W the epilogue applies at M == 1 (mvlm_gemv_ex). */
+int mvlm_gemm_packed_ex(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, const mvlm_weight* W,
+                        mvlm_buffer* C, int c_dtype, int M, int N, int K, const mvlm_epilogue* ep,
+                        mvlm_event** ev);
+int mvlm_gemv_ex(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W,
+                 mvlm_buffer* y, int y_dtype, int N, int K, const mvlm_epilogue* ep, mvlm_event** ev);
+
 /* ---- grouped decode GEMV ----------------------------------------------------
  * Up to MVLM_MAX_GROUP independent GEMVs (M = 1) in one launch, e.g. the
  * projections of one Phi-1.5 block that do not depend on each other: QKV and
@@ -223,6 +255,11 @@ int mvlm_plan_size(const mvlm_plan* plan);
 int mvlm_plan_add_gemv(mvlm_plan* plan, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W,
                        mvlm_buffer* y, int y_dtype, int M);
 int mvlm_plan_add_gemv_grouped(mvlm_plan* plan, int count, const mvlm_gemv_desc* descs);
+/* plan entries with a fused epilogue (mvlm_gemv_ex, M == 1; mvlm_gemm_packed_ex) */
+int mvlm_plan_add_gemv_ex(mvlm_plan* plan, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W,
+                          mvlm_buffer* y, int y_dtype, const mvlm_epilogue* ep);
+int mvlm_plan_add_gemm_packed_ex(mvlm_plan* plan, const mvlm_buffer* A, int a_dtype, const mvlm_weight* W,
+                                 mvlm_buffer* C, int c_dtype, int M, const mvlm_epilogue* ep);
 int mvlm_plan_add_gemm_packed(mvlm_plan* plan, const mvlm_buffer* A, int a_dtype, const mvlm_weight* W,
                               mvlm_buffer* C, int c_dtype, int M);
 int mvlm_plan_add_gemm_batched(mvlm_plan* plan, const mvlm_buffer* A, const mvlm_buffer* B,

@@ -120,7 +120,20 @@ inline void launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint3
         hipLaunchKernelGGL(kernel, grid, block, shmem, s, std::forward<Args>(args)...);
 }
 
+// Fused epilogue of a GEMM / GEMV store (mvlm_epilogue in mvlm_hip.h):
+// out = act(acc + bias[n]) * mul[i] + res[i], i the output element's index;
+// bias, mul and res have the output's dtype.
+struct Epilogue {
+    const void* bias = nullptr;
+    const void* mul = nullptr;
+    const void* res = nullptr;
+    int act = 0;
+    int dtype = 0;
+    bool any() const { return bias || mul || res || act; }
+};
+
 // Kernel launchers (defined in the .hip files).  They assume validated input.
+// A null Epilogue pointer means none.
 hipError_t launch_gemm_naive(hipStream_t s, const uint16_t* A, const uint16_t* B, uint16_t* C,
                              int M, int N, int K);
 hipError_t launch_gemm_tiled(hipStream_t s, const uint16_t* A, const uint16_t* B, uint16_t* C,
@@ -129,18 +142,19 @@ hipError_t launch_gemv_dense(hipStream_t s, const void* x, int x_dtype, const mv
                              void* y, int y_dtype, int N, int K);
 // Q8_0 / Q4_0 skinny GEMM on the matrix cores, 1 <= M <= 16 (any row length)
 hipError_t launch_gemm_skinny(hipStream_t s, const float* X, const mvlm_weight* W, float* Y, int M, int N, int K,
-                              int num_cus);
+                              int num_cus, const Epilogue* ep = nullptr);
 // M == 1 streaming GEMV for every weight format (rows of at most 16 KiB).
 bool stream_supported(const mvlm_weight* w);
 hipError_t launch_gemv_stream(hipStream_t s, const void* x, int x_dtype, const mvlm_weight* W, void* y,
-                              int y_dtype, int num_cus);
+                              int y_dtype, int num_cus, const Epilogue* ep = nullptr);
 hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const* xs, int x_dtype,
-                                    const mvlm_weight* const* ws, void* const* ys, const int* y_dtypes, int num_cus);
+                                    const mvlm_weight* const* ws, void* const* ys, const int* y_dtypes, int num_cus,
+                                    const Epilogue* eps = nullptr);
 inline int64_t weight_row_bytes(const mvlm_weight* w) { return is_dense(w->dtype) ? w->ld * (int64_t)dtype_size(w->dtype) : w->ld; }
 hipError_t launch_gemm_mfma(hipStream_t s, const void* A, int ab_dtype, const void* B, void* C,
                             int c_dtype, int batch, int M, int N, int K, int64_t lda, int64_t ldb,
                             int64_t ldc, int64_t strideA, int64_t strideB, int64_t strideC,
-                            int kread_b, int num_cus);
+                            int kread_b, int num_cus, const Epilogue* ep = nullptr);
 hipError_t launch_pack(hipStream_t s, const void* src, int dtype, int layout, int N, int K,
                        mvlm_weight* w);
 hipError_t launch_dequant(hipStream_t s, const mvlm_weight* w, float* out);

@@ -65,6 +65,33 @@ __device__ __forceinline__ void store_out(void* y, int64_t i, float v, int dtype
     else ((uint16_t*)y)[i] = f32_to_bf16_bits(v);             // MVLM_BF16
 }
 
+__device__ __forceinline__ float load_as_f32(const void* p, int64_t i, int dtype) {
+    if (dtype == 0) return ((const float*)p)[i];
+    const uint16_t h = ((const uint16_t*)p)[i];
+    return dtype == 1 ? f16_bits_to_f32(h) : bf16_bits_to_f32(h);
+}
+
+// 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), the tanh form of GELU
+// (src/kernels/activations.cl:68)
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float u = 0.7978845608f * __builtin_fmaf(0.044715f, x * x * x, x);
+    return 0.5f * x * (1.0f + tanhf(u));
+}
+
+// x / (1 + exp(-x))  (src/kernels/activations.cl:22)
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+// out = act(v + bias[n]) * mul[i] + res[i]  (Epilogue, common.h)
+template <class E>
+__device__ __forceinline__ float apply_epilogue(const E& e, float v, int64_t i, int64_t n) {
+    if (e.bias) v += load_as_f32(e.bias, n, e.dtype);
+    if (e.act == 1) v = gelu_tanh(v);
+    else if (e.act == 2) v = silu(v);
+    if (e.mul) v *= load_as_f32(e.mul, i, e.dtype);
+    if (e.res) v += load_as_f32(e.res, i, e.dtype);
+    return v;
+}
+
 // Sum over the 64 lanes of a wavefront; every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -51,6 +51,8 @@ struct GemmArgs {
     int64_t lda, ldb, ldc, sA, sB, sC;
     int kread_b;        // B rows are readable (zero padded) up to this K (>= K)
     int tiles_m, tiles_n;
+    Epilogue ep;        // applied when ep_on (mul / res indexed like C)
+    int ep_on;
 };
 
 template <bool BF16>
@@ -233,18 +235,36 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(const GemmArg
     }
 
     const int64_t c_off = (int64_t)blockIdx.z * p.sC;
+    if (!p.ep_on) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int col = n0 + wn * WN + j * 32 + (lane & 31);
-            if (col >= p.N) continue;
+            for (int j = 0; j < TN; ++j) {
+                const int col = n0 + wn * WN + j * 32 + (lane & 31);
+                if (col >= p.N) continue;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (row < p.M) store_out(p.C, c_off + (int64_t)row * p.ldc + col, acc[i][j][r], p.c_dtype);
+                for (int r = 0; r < 16; ++r) {
+                    const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    if (row < p.M) store_out(p.C, c_off + (int64_t)row * p.ldc + col, acc[i][j][r], p.c_dtype);
+                }
             }
-        }
+    } else {   // fused epilogue: the per-element code is larger, so only the tile loops unroll
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int col = n0 + wn * WN + j * 32 + (lane & 31);
+                if (col >= p.N) continue;
+#pragma unroll 4
+                for (int r = 0; r < 16; ++r) {
+                    const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    if (row < p.M) {
+                        const int64_t idx = c_off + (int64_t)row * p.ldc + col;
+                        store_out(p.C, idx, apply_epilogue(p.ep, acc[i][j][r], idx, col), p.c_dtype);
+                    }
+                }
+            }
+    }
 }
 
 // ---- launch configuration ----------------------------------------------------
@@ -299,12 +319,17 @@ static const TileCfg& pick_tile(int M, int N, int batch, int num_cus) {
 
 hipError_t launch_gemm_mfma(hipStream_t s, const void* A, int ab_dtype, const void* B, void* C, int c_dtype,
                             int batch, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
-                            int64_t strideA, int64_t strideB, int64_t strideC, int kread_b, int num_cus) {
+                            int64_t strideA, int64_t strideB, int64_t strideC, int kread_b, int num_cus,
+                            const Epilogue* ep) {
     GemmArgs a{};
     a.A = (const uint16_t*)A; a.B = (const uint16_t*)B; a.C = C; a.c_dtype = c_dtype;
     a.M = M; a.N = N; a.K = K; a.lda = lda; a.ldb = ldb; a.ldc = ldc;
     a.sA = strideA; a.sB = strideB; a.sC = strideC;
     a.kread_b = kread_b;
+    if (ep && ep->any()) {
+        a.ep = *ep;
+        a.ep_on = 1;
+    }
     const TileCfg& t = pick_tile(M, N, batch, num_cus > 0 ? num_cus : 256);
     a.tiles_m = (M + t.bm - 1) / t.bm;
     a.tiles_n = (N + t.bn - 1) / t.bn;

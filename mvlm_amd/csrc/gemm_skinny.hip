@@ -120,7 +120,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(const float* __res
                                                               const uint8_t* __restrict__ codes,
                                                               const uint16_t* __restrict__ scales,
                                                               float* __restrict__ Y, int M, int N, int K,
-                                                              int64_t ld) {
+                                                              int64_t ld, const Epilogue ep, int ep_on) {
     using L = SkinnyLayout<Q4>;
     constexpr int ROWS = 16 * R;
     constexpr int SLOT = skinny_slot_bytes<Q4, R, NW>();
@@ -275,14 +275,18 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(const float* __res
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int m = 4 * q + i;
-                if (m < M) Y[(int64_t)m * N + n] = sum[i];
+                if (m < M) {
+                    const int64_t idx = (int64_t)m * N + n;
+                    Y[idx] = ep_on ? apply_epilogue(ep, sum[i], idx, n) : sum[i];
+                }
             }
         }
     }
 }
 
 template <bool Q4, int R, int NW>
-static hipError_t launch_skinny(hipStream_t s, const float* X, const mvlm_weight* W, float* Y, int M, int N, int K) {
+static hipError_t launch_skinny(hipStream_t s, const float* X, const mvlm_weight* W, float* Y, int M, int N, int K,
+                                const Epilogue& ep) {
     auto kernel = gemm_skinny_kernel<Q4, R, NW>;
     const size_t lds = skinny_lds_bytes<Q4, R, NW>(K);
     static bool attr_set = false;
@@ -295,7 +299,7 @@ static hipError_t launch_skinny(hipStream_t s, const float* X, const mvlm_weight
     if (lds > SKINNY_LDS_MAX) return hipErrorInvalidValue;
     const unsigned blocks = (unsigned)((N + 16 * R - 1) / (16 * R));
     launch_kernel(kernel, dim3(blocks), dim3(64 * NW), (uint32_t)lds, s, X, (const uint8_t*)W->data,
-                  (const uint16_t*)W->scales, Y, M, N, K, (int64_t)W->ld);
+                  (const uint16_t*)W->scales, Y, M, N, K, (int64_t)W->ld, ep, ep.any() ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -303,19 +307,21 @@ static hipError_t launch_skinny(hipStream_t s, const float* X, const mvlm_weight
 // row groups than CUs get 16-wave blocks (more loads in flight per block).
 template <bool Q4>
 static hipError_t launch_skinny_shape(hipStream_t s, const float* X, const mvlm_weight* W, float* Y, int M, int N,
-                                      int K, int num_cus) {
+                                      int K, int num_cus, const Epilogue& ep) {
     const int groups = (N + 15) / 16;
-    if (groups >= 2 * num_cus) return launch_skinny<Q4, 2, 8>(s, X, W, Y, M, N, K);
-    if (groups >= num_cus) return launch_skinny<Q4, 1, 8>(s, X, W, Y, M, N, K);
-    return launch_skinny<Q4, 1, 16>(s, X, W, Y, M, N, K);
+    if (groups >= 2 * num_cus) return launch_skinny<Q4, 2, 8>(s, X, W, Y, M, N, K, ep);
+    if (groups >= num_cus) return launch_skinny<Q4, 1, 8>(s, X, W, Y, M, N, K, ep);
+    return launch_skinny<Q4, 1, 16>(s, X, W, Y, M, N, K, ep);
 }
 
 hipError_t launch_gemm_skinny(hipStream_t s, const float* X, const mvlm_weight* W, float* Y, int M, int N, int K,
-                              int num_cus) {
+                              int num_cus, const Epilogue* ep) {
     if (M < 1 || M > 16 || K % 32 != 0 || !is_quant(W->dtype)) return hipErrorInvalidValue;
     if (num_cus <= 0) num_cus = 256;
-    if (W->dtype == MVLM_Q4_0) return launch_skinny_shape<true>(s, X, W, Y, M, N, K, num_cus);
-    return launch_skinny_shape<false>(s, X, W, Y, M, N, K, num_cus);
+    const Epilogue none{};
+    const Epilogue& e = ep ? *ep : none;
+    if (W->dtype == MVLM_Q4_0) return launch_skinny_shape<true>(s, X, W, Y, M, N, K, num_cus, e);
+    return launch_skinny_shape<false>(s, X, W, Y, M, N, K, num_cus, e);
 }
 
 }  // namespace mvlm

@@ -158,6 +158,8 @@ struct StreamProblem {
     int shape;                     // index into kShapes
     int rows_per_block;            // block j owns rows [j*rows_per_block, (j+1)*rows_per_block) below N
     int block_begin;               // first block of this problem in the grid
+    int ep_on;
+    Epilogue ep;                   // applied to y when ep_on
 };
 
 constexpr int MAX_GROUP = 8;
@@ -256,7 +258,9 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
         if (lane == 0 && active) {
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                if (row0 + r < rb1) store_out(P.y, row0 + r, acc[r], P.y_dtype);
+                if (row0 + r < rb1)
+                    store_out(P.y, row0 + r, P.ep_on ? apply_epilogue(P.ep, acc[r], row0 + r, row0 + r) : acc[r],
+                              P.y_dtype);
         }
     } else {
         if (lane == 0) {
@@ -270,7 +274,8 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
                 float v = part[wave][r];
 #pragma unroll
                 for (int s = 1; s < SPLIT; ++s) v += part[wave + s][r];
-                if (row0 + r < rb1) store_out(P.y, row0 + r, v, P.y_dtype);
+                if (row0 + r < rb1)
+                    store_out(P.y, row0 + r, P.ep_on ? apply_epilogue(P.ep, v, row0 + r, row0 + r) : v, P.y_dtype);
             }
         }
     }
@@ -410,7 +415,8 @@ static hipError_t launch_group_x(hipStream_t s, int x_dtype, StreamGroup& g, siz
 
 // All problems share the weight dtype and x dtype (checked by the caller).
 hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const* xs, int x_dtype,
-                                    const mvlm_weight* const* ws, void* const* ys, const int* y_dtypes, int num_cus) {
+                                    const mvlm_weight* const* ws, void* const* ys, const int* y_dtypes, int num_cus,
+                                    const Epilogue* eps) {
     if (count < 1 || count > MAX_GROUP) return hipErrorInvalidValue;
     StreamGroup g{};
     g.count = count;
@@ -428,6 +434,10 @@ hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const*
         p.K = w->K;
         p.y_dtype = y_dtypes[i];
         p.shape = stream_shape(w);
+        if (eps && eps[i].any()) {
+            p.ep = eps[i];
+            p.ep_on = 1;
+        }
         if (p.shape < 0) return hipErrorInvalidValue;
         const size_t b = stream_lds_bytes(w, x_dtype, p.shape);
         lds = b > lds ? b : lds;
@@ -445,8 +455,8 @@ hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const*
 }
 
 hipError_t launch_gemv_stream(hipStream_t s, const void* x, int x_dtype, const mvlm_weight* W, void* y,
-                              int y_dtype, int num_cus) {
-    return launch_gemv_stream_group(s, 1, &x, x_dtype, &W, &y, &y_dtype, num_cus);
+                              int y_dtype, int num_cus, const Epilogue* ep) {
+    return launch_gemv_stream_group(s, 1, &x, x_dtype, &W, &y, &y_dtype, num_cus, ep);
 }
 
 }  // namespace mvlm

@@ -34,6 +34,7 @@ struct Op {
     const mvlm_weight* gw[MVLM_MAX_GROUP] = {};
     void* gy[MVLM_MAX_GROUP] = {};
     int gyd[MVLM_MAX_GROUP] = {};
+    Epilogue ep;                  // fused epilogue (GEMM MFMA, GEMV)
 };
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -49,6 +50,34 @@ int need(const mvlm_buffer* b, size_t bytes, const char* fn, const char* name) {
         int _st = need((buf), (bytes), fn, (name));              \
         if (_st != MVLM_OK) return _st;                          \
     } while (0)
+
+// Validates a caller's epilogue for an [M][N] output of dtype c_dtype.
+int make_epilogue(mvlm_device* dev, const mvlm_epilogue* in, int M, int N, int c_dtype, const char* fn,
+                  Epilogue* out) {
+    *out = Epilogue{};
+    if (!in) return MVLM_OK;
+    REQUIRE(in->activation >= MVLM_ACT_NONE && in->activation <= MVLM_ACT_SILU, "%s: unknown activation %d", fn,
+            in->activation);
+    const size_t es = dtype_size(c_dtype);
+    if (in->bias) {
+        REQUIRE(in->bias->dev == dev, "%s: bias belongs to another device", fn);
+        NEED(in->bias, (size_t)N * es, "bias");
+        out->bias = in->bias->ptr;
+    }
+    if (in->mul) {
+        REQUIRE(in->mul->dev == dev, "%s: mul belongs to another device", fn);
+        NEED(in->mul, (size_t)M * N * es, "mul");
+        out->mul = in->mul->ptr;
+    }
+    if (in->residual) {
+        REQUIRE(in->residual->dev == dev, "%s: residual belongs to another device", fn);
+        NEED(in->residual, (size_t)M * N * es, "residual");
+        out->res = in->residual->ptr;
+    }
+    out->act = in->activation;
+    out->dtype = c_dtype;
+    return MVLM_OK;
+}
 
 int make_ref_gemm(OpKind kind, mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer* B, mvlm_buffer* C,
                   int M, int N, int K, const char* fn, Op* op) {
@@ -180,15 +209,16 @@ hipError_t enqueue_op(hipStream_t s, const Op& op) {
             return launch_gemm_tiled(s, (const uint16_t*)op.a, (const uint16_t*)op.b, (uint16_t*)op.c, op.M, op.N, op.K);
         case OP_GEMM_MFMA:
             return launch_gemm_mfma(s, op.a, op.a_dtype, op.b, op.c, op.c_dtype, op.batch, op.M, op.N, op.K,
-                                    op.lda, op.ldb, op.ldc, op.sA, op.sB, op.sC, op.kread_b, op.num_cus);
+                                    op.lda, op.ldb, op.ldc, op.sA, op.sB, op.sC, op.kread_b, op.num_cus, &op.ep);
         case OP_GEMV_DENSE:
             if (stream_supported(op.w))
-                return launch_gemv_stream(s, op.a, op.a_dtype, op.w, op.c, op.c_dtype, op.num_cus);
+                return launch_gemv_stream(s, op.a, op.a_dtype, op.w, op.c, op.c_dtype, op.num_cus, &op.ep);
             return launch_gemv_dense(s, op.a, op.a_dtype, op.w, op.c, op.c_dtype, op.N, op.K);
         case OP_GEMV_QUANT:
             if (op.M == 1 && stream_supported(op.w))
-                return launch_gemv_stream(s, op.a, MVLM_F32, op.w, op.c, MVLM_F32, op.num_cus);
-            return launch_gemm_skinny(s, (const float*)op.a, op.w, (float*)op.c, op.M, op.N, op.K, op.num_cus);
+                return launch_gemv_stream(s, op.a, MVLM_F32, op.w, op.c, MVLM_F32, op.num_cus, &op.ep);
+            return launch_gemm_skinny(s, (const float*)op.a, op.w, (float*)op.c, op.M, op.N, op.K, op.num_cus,
+                                      &op.ep);
     }
     return hipErrorInvalidValue;
 }
@@ -206,6 +236,12 @@ int run_one(mvlm_device* dev, const Op& op, mvlm_event** ev, const char* fn) {
 // ---------------------------------------------------------------------------
 // direct entry points
 // ---------------------------------------------------------------------------
+
+// the second step of a two-step op construction, run only if the first succeeded
+template <class F>
+int then(int st, F&& next) {
+    return st != MVLM_OK ? st : next();
+}
 
 #define RUN(make_call)                                 \
     do {                                               \
@@ -234,6 +270,14 @@ extern "C" int mvlm_gemm_packed(mvlm_device* dev, const mvlm_buffer* A, int a_dt
     RUN(make_gemm_packed(dev, A, a_dtype, W, C, c_dtype, M, N, K, fn, &op));
 }
 
+extern "C" int mvlm_gemm_packed_ex(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, const mvlm_weight* W,
+                                   mvlm_buffer* C, int c_dtype, int M, int N, int K, const mvlm_epilogue* ep,
+                                   mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(then(make_gemm_packed(dev, A, a_dtype, W, C, c_dtype, M, N, K, fn, &op),
+             [&] { return make_epilogue(dev, ep, M, N, c_dtype, fn, &op.ep); }));
+}
+
 extern "C" int mvlm_gemm_batched(mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer* B, mvlm_buffer* C,
                                  int batch, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
                                  int64_t strideA, int64_t strideB, int64_t strideC, mvlm_event** ev) {
@@ -245,6 +289,13 @@ extern "C" int mvlm_gemv(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, co
                          mvlm_buffer* y, int y_dtype, int N, int K, mvlm_event** ev) {
     const char* fn = __func__;
     RUN(make_gemv(dev, x, x_dtype, W, y, y_dtype, 1, N, K, -1, fn, &op));
+}
+
+extern "C" int mvlm_gemv_ex(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W,
+                            mvlm_buffer* y, int y_dtype, int N, int K, const mvlm_epilogue* ep, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(then(make_gemv(dev, x, x_dtype, W, y, y_dtype, 1, N, K, -1, fn, &op),
+             [&] { return make_epilogue(dev, ep, 1, N, y_dtype, fn, &op.ep); }));
 }
 
 extern "C" int mvlm_gemv_grouped(mvlm_device* dev, int count, const mvlm_gemv_desc* descs, mvlm_event** ev) {
@@ -329,6 +380,27 @@ extern "C" int mvlm_plan_add_gemv(mvlm_plan* plan, const mvlm_buffer* x, int x_d
     REQUIRE(plan && W, "%s: null argument", fn);
     Op op{};
     int st = make_gemv(plan->dev, x, x_dtype, W, y, y_dtype, M, W->N, W->K, -1, fn, &op);
+    return st != MVLM_OK ? st : plan_push(plan, op);
+}
+
+extern "C" int mvlm_plan_add_gemv_ex(mvlm_plan* plan, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W,
+                                     mvlm_buffer* y, int y_dtype, const mvlm_epilogue* ep) {
+    const char* fn = __func__;
+    REQUIRE(plan && W, "%s: null argument", fn);
+    Op op{};
+    int st = make_gemv(plan->dev, x, x_dtype, W, y, y_dtype, 1, W->N, W->K, -1, fn, &op);
+    if (st == MVLM_OK) st = make_epilogue(plan->dev, ep, 1, W->N, y_dtype, fn, &op.ep);
+    return st != MVLM_OK ? st : plan_push(plan, op);
+}
+
+extern "C" int mvlm_plan_add_gemm_packed_ex(mvlm_plan* plan, const mvlm_buffer* A, int a_dtype,
+                                            const mvlm_weight* W, mvlm_buffer* C, int c_dtype, int M,
+                                            const mvlm_epilogue* ep) {
+    const char* fn = __func__;
+    REQUIRE(plan && W, "%s: null argument", fn);
+    Op op{};
+    int st = make_gemm_packed(plan->dev, A, a_dtype, W, C, c_dtype, M, W->N, W->K, fn, &op);
+    if (st == MVLM_OK) st = make_epilogue(plan->dev, ep, M, W->N, c_dtype, fn, &op.ep);
     return st != MVLM_OK ? st : plan_push(plan, op);
 }
 

@@ -49,6 +49,18 @@ class GgufTensor(ctypes.Structure):
                 ("dims", c_uint64 * 4), ("type", ctypes.c_uint32), ("offset", c_uint64), ("bytes", c_uint64)]
 
 
+ACT_NONE, ACT_GELU_TANH, ACT_SILU = 0, 1, 2
+
+
+class Epilogue(ctypes.Structure):
+    _fields_ = [("bias", c_void_p), ("activation", c_int), ("mul", c_void_p), ("residual", c_void_p)]
+
+
+def _epilogue(bias=None, act=ACT_NONE, mul=None, residual=None):
+    return Epilogue(bias.handle if bias is not None else None, act,
+                    mul.handle if mul is not None else None, residual.handle if residual is not None else None)
+
+
 class GemvDesc(ctypes.Structure):
     _fields_ = [("x", c_void_p), ("x_dtype", c_int), ("W", c_void_p), ("y", c_void_p), ("y_dtype", c_int)]
 
@@ -89,6 +101,10 @@ _SIGNATURES = {
     "mvlm_gemm_packed": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, c_int, c_int, _PP]),
     "mvlm_gemv": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, c_int, _PP]),
     "mvlm_gemv_grouped": (c_int, [_P, c_int, POINTER(GemvDesc), _PP]),
+    "mvlm_gemm_packed_ex": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, c_int, c_int, POINTER(Epilogue), _PP]),
+    "mvlm_gemv_ex": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, c_int, POINTER(Epilogue), _PP]),
+    "mvlm_plan_add_gemv_ex": (c_int, [_P, _P, c_int, _P, _P, c_int, POINTER(Epilogue)]),
+    "mvlm_plan_add_gemm_packed_ex": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, POINTER(Epilogue)]),
     "mvlm_plan_add_gemv_grouped": (c_int, [_P, c_int, POINTER(GemvDesc)]),
     "mvlm_gemv_q8_0": (c_int, [_P, _P, _P, _P, c_int, c_int, _PP]),
     "mvlm_gemv_q4_0": (c_int, [_P, _P, _P, _P, c_int, c_int, _PP]),
@@ -382,6 +398,19 @@ class Plan:
             self._keep += [x, W, y]
         return self
 
+    def add_gemv_ex(self, x, x_dtype, W, y, y_dtype, bias=None, act=ACT_NONE, mul=None, residual=None):
+        ep = _epilogue(bias, act, mul, residual)
+        _call("mvlm_plan_add_gemv_ex", self.handle, x.handle, x_dtype, W.handle, y.handle, y_dtype, byref(ep))
+        self._keep += [x, W, y] + [b for b in (bias, mul, residual) if b is not None]
+        return self
+
+    def add_gemm_packed_ex(self, A, a_dtype, W, C, c_dtype, M, bias=None, act=ACT_NONE, mul=None, residual=None):
+        ep = _epilogue(bias, act, mul, residual)
+        _call("mvlm_plan_add_gemm_packed_ex", self.handle, A.handle, a_dtype, W.handle, C.handle, c_dtype, M,
+              byref(ep))
+        self._keep += [A, W, C] + [b for b in (bias, mul, residual) if b is not None]
+        return self
+
     def add_gemm_packed(self, A, a_dtype, W, C, c_dtype, M):
         _call("mvlm_plan_add_gemm_packed", self.handle, A.handle, a_dtype, W.handle, C.handle, c_dtype, M)
         self._keep += [A, W, C]
@@ -498,6 +527,17 @@ class Device:
 
     def gemm_packed(self, A, a_dtype, W, C, c_dtype, M, N, K, event=False):
         return self._launch("mvlm_gemm_packed", (A.handle, a_dtype, W.handle, C.handle, c_dtype, M, N, K), event)
+
+    def gemm_packed_ex(self, A, a_dtype, W, C, c_dtype, M, N, K, bias=None, act=ACT_NONE, mul=None, residual=None,
+                       event=False):
+        ep = _epilogue(bias, act, mul, residual)
+        return self._launch("mvlm_gemm_packed_ex", (A.handle, a_dtype, W.handle, C.handle, c_dtype, M, N, K,
+                                                     byref(ep)), event)
+
+    def gemv_ex(self, x, x_dtype, W, y, y_dtype, N, K, bias=None, act=ACT_NONE, mul=None, residual=None,
+                event=False):
+        ep = _epilogue(bias, act, mul, residual)
+        return self._launch("mvlm_gemv_ex", (x.handle, x_dtype, W.handle, y.handle, y_dtype, N, K, byref(ep)), event)
 
     def gemv(self, x, x_dtype, W, y, y_dtype, N, K, event=False):
         return self._launch("mvlm_gemv", (x.handle, x_dtype, W.handle, y.handle, y_dtype, N, K), event)

@@ -451,3 +451,27 @@ void orc_gemm_f64_nk(const double* X, const double* W, double* Y, double* S,
             if (S) S[(size_t)m * N + n] = s;
         }
 }
+
+/* ---- fused epilogue -------------------------------------------------------
+ * activations.cl:66-118 (gelu), :22-60 (silu), vision.cl:178-186 / 433-436
+ * (bias), activations.cl:259-290 (vector_add residual), :204-255 (gate). */
+double orc_gelu_tanh(double x) {
+    const double c = sqrt(2.0 / 3.14159265358979323846);
+    return 0.5 * x * (1.0 + tanh(c * (x + 0.044715 * x * x * x)));
+}
+
+double orc_silu(double x) { return x / (1.0 + exp(-x)); }
+
+void orc_epilogue_f64(double* Y, const double* bias, const double* mul, const double* res, int act, int M, int N) {
+    for (int m = 0; m < M; ++m)
+        for (int n = 0; n < N; ++n) {
+            const size_t i = (size_t)m * N + n;
+            double v = Y[i];
+            if (bias) v += bias[n];
+            if (act == 1) v = orc_gelu_tanh(v);
+            else if (act == 2) v = orc_silu(v);
+            if (mul) v *= mul[i];
+            if (res) v += res[i];
+            Y[i] = v;
+        }
+}

@@ -100,6 +100,14 @@ void orc_gemm_batched_f16(const uint16_t* A, const uint16_t* B, float* C, int ba
 void orc_gemm_f64_nk(const double* X, const double* W, double* Y, double* S,
                      int M, int N, int K, int nthreads);
 
+/* ---- fused epilogue: Y[i] = act(Y[i] + bias[n]) * mul[i] + res[i] (fp64) -
+ * act 0: none; 1: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
+ * (src/kernels/activations.cl:68, the formula its comment states);
+ * 2: x / (1 + exp(-x)) (activations.cl:22).  bias/mul/res may be NULL. */
+double orc_gelu_tanh(double x);
+double orc_silu(double x);
+void orc_epilogue_f64(double* Y, const double* bias, const double* mul, const double* res, int act, int M, int N);
+
 int orc_max_threads(void);
 
 #ifdef __cplusplus

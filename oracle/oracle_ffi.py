@@ -69,6 +69,9 @@ def lib():
                                             ctypes.c_long, ctypes.c_long, ctypes.c_long]),
             "orc_gemm_f64_nk": (None, [_f64p, _f64p, _f64p, _f64p, i, i, i, i]),
             "orc_max_threads": (i, []),
+            "orc_gelu_tanh": (d, [d]),
+            "orc_silu": (d, [d]),
+            "orc_epilogue_f64": (None, [_f64p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, i, i, i]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -204,6 +207,23 @@ def gemm_f64(X, W, M, N, K, nthreads=0):
     lib().orc_gemm_f64_nk(np.ascontiguousarray(X, np.float64).ravel(),
                           np.ascontiguousarray(W, np.float64).ravel(), Y, S, M, N, K, nthreads)
     return Y.reshape(M, N), S.reshape(M, N)
+
+
+def epilogue_f64(Y, bias=None, mul=None, res=None, act=0):
+    """Y[M,N] (fp64, updated copy) -> act(Y + bias[n]) * mul + res."""
+    Y = np.array(Y, np.float64, copy=True)
+    M, N = Y.shape
+
+    def ptr(a, n):
+        if a is None:
+            return None
+        a = np.ascontiguousarray(a, np.float64).ravel()
+        assert a.size == n
+        keep.append(a)
+        return a.ctypes.data
+    keep = []
+    lib().orc_epilogue_f64(Y.ravel(), ptr(bias, N), ptr(mul, M * N), ptr(res, M * N), act, M, N)
+    return Y
 
 
 def gemm_batched_f16(A, B, batch, M, N, K, lda, ldb, ldc, sA, sB, sC, c_elems):

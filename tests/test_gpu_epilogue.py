@@ -1,0 +1,187 @@
+"""Fused epilogues (mvlm_epilogue): out = act(acc + bias[n]) * mul + residual,
+applied in the store of the MFMA GEMM, the streaming GEMV (M = 1) and the
+long-row skinny path, checked against the oracle's fp64 GEMM followed by its
+fp64 epilogue (oracle/oracle.c orc_epilogue_f64: the formulas of
+activations.cl:22 and :68, bias as vision.cl:178-186, residual as
+activations.cl:259-290).
+
+Tolerance per element: the accumulator's bound (rtol * S, S = sum |x*w|)
+carried through the activation (slope <= 1.2) and the gate factor, plus a
+few fp32 ulps of the epilogue arithmetic, plus half an ulp of the output
+dtype."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import mvlm_amd as m
+from mvlm_amd import native
+
+pytestmark = pytest.mark.gpu
+
+F32, F16, BF16 = m.F32, m.F16, m.BF16
+NONE, GELU, SILU = native.ACT_NONE, native.ACT_GELU_TANH, native.ACT_SILU
+
+
+def to_storage(orc, v32, dt):
+    """fp32 values -> (bits or floats in the dtype's storage, their exact fp64 values)."""
+    v32 = np.ascontiguousarray(v32, np.float32)
+    if dt == F32:
+        return v32, v32.astype(np.float64)
+    if dt == F16:
+        bits = np.empty(v32.size, np.uint16)
+        orc.lib().orc_f32_to_f16_array(v32, bits, v32.size)
+        back = np.empty(v32.size, np.float32)
+        orc.lib().orc_f16_to_f32_array(bits, back, v32.size)
+        return bits, back.astype(np.float64)
+    bits = np.empty(v32.size, np.uint16)
+    orc.lib().orc_f32_to_bf16_array(v32, bits, v32.size)
+    back = np.empty(v32.size, np.float32)
+    orc.lib().orc_bf16_to_f32_array(bits, back, v32.size)
+    return bits, back.astype(np.float64)
+
+
+def from_storage(orc, raw, dt):
+    if dt == F32:
+        return raw.astype(np.float64)
+    back = np.empty(raw.size, np.float32)
+    (orc.lib().orc_f16_to_f32_array if dt == F16 else orc.lib().orc_bf16_to_f32_array)(
+        np.ascontiguousarray(raw, np.uint16), back, raw.size)
+    return back.astype(np.float64)
+
+
+def half_ulp(v, dt):
+    mant = {F32: 24, F16: 11, BF16: 8}[dt]
+    return np.abs(v) * 2.0 ** -mant + (6e-8 if dt == F16 else 0.0)
+
+
+def make_operands(dev, orc, M, N, dt, seed, bias, mul, residual):
+    rng = np.random.default_rng(seed)
+    ops, vals = {}, {}
+    for name, want, shape in (("bias", bias, N), ("mul", mul, M * N), ("residual", residual, M * N)):
+        if want:
+            raw, v = to_storage(orc, rng.standard_normal(shape).astype(np.float32), dt)
+            ops[name] = dev.upload(raw)
+            vals[name] = v
+        else:
+            ops[name] = None
+            vals[name] = None
+    return ops, vals
+
+
+def check(orc, got, Y64, S, vals, act, dt, rtol):
+    M, N = Y64.shape
+    ref = orc.epilogue_f64(Y64, vals["bias"], None if vals["mul"] is None else vals["mul"].reshape(M, N),
+                           None if vals["residual"] is None else vals["residual"].reshape(M, N), act)
+    gate = np.ones((M, N)) if vals["mul"] is None else np.abs(vals["mul"].reshape(M, N))
+    res = np.zeros((M, N)) if vals["residual"] is None else np.abs(vals["residual"].reshape(M, N))
+    body = orc.epilogue_f64(Y64, vals["bias"], act=act)
+    tol = rtol * S * 1.2 * gate + 4e-6 * (np.abs(body) * gate + res) + half_ulp(ref, dt) + 1e-30
+    err = np.abs(got - ref)
+    assert np.all(err <= tol), float(np.max(err / tol))
+
+
+EPILOGUES = [(True, NONE, False, False), (True, GELU, False, False), (False, SILU, True, False),
+             (True, NONE, False, True), (True, GELU, True, True), (False, SILU, False, True)]
+
+
+@pytest.mark.parametrize("bias,act,mul,residual", EPILOGUES)
+@pytest.mark.parametrize("cd", [F32, F16, BF16])
+def test_gemm_packed_epilogue(dev, orc, bias, act, mul, residual, cd):
+    M, N, K = 129, 200, 256
+    A = orc.normal_f16(M * K, 0x71)
+    Wt = orc.normal_f16(N * K, 0x72, 0.05)
+    W = dev.pack(Wt, F16, N, K)
+    ops, vals = make_operands(dev, orc, M, N, cd, 0x73, bias, mul, residual)
+    dA, dC = dev.upload(A), dev.alloc(M * N * 4)
+    dev.gemm_packed_ex(dA, F16, W, dC, cd, M, N, K, bias=ops["bias"], act=act, mul=ops["mul"],
+                       residual=ops["residual"])
+    got = from_storage(orc, dC.download(np.float32 if cd == F32 else np.uint16, M * N), cd).reshape(M, N)
+    A64 = from_storage(orc, A, F16).reshape(M, K)
+    W64 = from_storage(orc, Wt, F16).reshape(N, K)
+    Y64, S = orc.gemm_f64(A64, W64, M, N, K)
+    check(orc, got, Y64, S, vals, act, cd, 1e-4)
+
+
+def test_gemm_epilogue_residual_in_place(dev, orc):
+    """residual aliasing the output: C = gelu(A W^T + b) + C"""
+    M, N, K = 64, 96, 128
+    A = orc.normal_f16(M * K, 0x74)
+    Wt = orc.normal_f16(N * K, 0x75, 0.05)
+    W = dev.pack(Wt, F16, N, K)
+    ops, vals = make_operands(dev, orc, M, N, F32, 0x76, True, False, True)
+    C = ops["residual"]
+    dev.gemm_packed_ex(dev.upload(A), F16, W, C, F32, M, N, K, bias=ops["bias"], act=GELU, residual=C)
+    got = C.download(np.float32, M * N).astype(np.float64).reshape(M, N)
+    Y64, S = orc.gemm_f64(from_storage(orc, A, F16).reshape(M, K), from_storage(orc, Wt, F16).reshape(N, K), M, N, K)
+    check(orc, got, Y64, S, vals, GELU, F32, 1e-4)
+
+
+@pytest.mark.parametrize("qt,N,K", [(m.Q8_0, 300, 2048), (m.Q4_0, 130, 8192), (m.Q8_0, 24, 20480)])
+@pytest.mark.parametrize("bias,act,mul,residual", [(True, GELU, False, False), (False, NONE, False, True),
+                                                   (True, SILU, True, True)])
+def test_quant_gemv_epilogue(dev, orc, qt, N, K, bias, act, mul, residual):
+    """streaming GEMV stores (the 20480-long rows take the skinny path)"""
+    x = orc.normal_f32(K, 0x77)
+    blocks = (orc.q8_0_blocks if qt == m.Q8_0 else orc.q4_0_blocks)(N * K // 32, 0x78)
+    W = dev.pack(blocks, qt, N, K)
+    ops, vals = make_operands(dev, orc, 1, N, F32, 0x79, bias, mul, residual)
+    y = dev.alloc(N * 4)
+    dev.gemv_ex(dev.upload(x), F32, W, y, F32, N, K, bias=ops["bias"], act=act, mul=ops["mul"],
+                residual=ops["residual"])
+    deq = (orc.dequant_q8_0 if qt == m.Q8_0 else orc.dequant_q4_0)(blocks).astype(np.float64).reshape(N, K)
+    Y64, S = orc.gemm_f64(x.astype(np.float64)[None], deq, 1, N, K)
+    check(orc, y.download(np.float32).astype(np.float64)[None], Y64, S, vals, act, F32, 1e-5)
+
+
+@pytest.mark.parametrize("yd", [F32, BF16])
+def test_dense_gemv_epilogue(dev, orc, yd):
+    N, K = 515, 1024
+    x = orc.normal_f16(K, 0x7A)
+    Wt = orc.normal_f16(N * K, 0x7B, 0.05)
+    W = dev.pack(Wt, F16, N, K)
+    ops, vals = make_operands(dev, orc, 1, N, yd, 0x7C, True, True, True)
+    y = dev.alloc(N * 4)
+    dev.gemv_ex(dev.upload(x), F16, W, y, yd, N, K, bias=ops["bias"], act=GELU, mul=ops["mul"],
+                residual=ops["residual"])
+    got = from_storage(orc, y.download(np.float32 if yd == F32 else np.uint16, N), yd)[None]
+    Y64, S = orc.gemm_f64(from_storage(orc, x, F16)[None], from_storage(orc, Wt, F16).reshape(N, K), 1, N, K)
+    check(orc, got, Y64, S, vals, GELU, yd, 1e-5)
+
+
+def test_plan_epilogues_match_direct_calls(dev, orc):
+    M, N, K = 33, 64, 2048
+    A = orc.normal_f16(M * K, 0x7D)
+    Wt = orc.normal_f16(N * K, 0x7E, 0.05)
+    W = dev.pack(Wt, F16, N, K)
+    Wq = dev.pack(orc.q8_0_blocks(N * K // 32, 0x7F), m.Q8_0, N, K)
+    x = dev.upload(orc.normal_f32(K, 0x80))
+    dA = dev.upload(A)
+    ops, _ = make_operands(dev, orc, M, N, F32, 0x81, True, True, True)
+    c1, c2, y1, y2 = (dev.alloc(M * N * 4) for _ in range(4))
+    dev.gemm_packed_ex(dA, F16, W, c1, F32, M, N, K, bias=ops["bias"], act=SILU, mul=ops["mul"],
+                       residual=ops["residual"])
+    dev.gemv_ex(x, F32, Wq, y1, F32, N, K, bias=ops["bias"], act=GELU)
+    plan = m.Plan(dev)
+    plan.add_gemm_packed_ex(dA, F16, W, c2, F32, M, bias=ops["bias"], act=SILU, mul=ops["mul"],
+                            residual=ops["residual"])
+    plan.add_gemv_ex(x, F32, Wq, y2, F32, bias=ops["bias"], act=GELU)
+    plan.use_graph(True)
+    plan.run(3)
+    dev.sync()
+    assert np.array_equal(c1.download(np.float32, M * N), c2.download(np.float32, M * N))
+    assert np.array_equal(y1.download(np.float32, N), y2.download(np.float32, N))
+    plan.destroy()
+
+
+def test_epilogue_argument_errors(dev, orc):
+    N, K = 64, 64
+    W = dev.pack(orc.normal_f16(N * K, 1), F16, N, K)
+    x, y = dev.upload(orc.normal_f16(K, 2)), dev.alloc(N * 4)
+    small = dev.alloc(8)
+    with pytest.raises(m.MvlmError) as e:
+        dev.gemv_ex(x, F16, W, y, F32, N, K, bias=small)
+    assert e.value.code == native.ERR_BUFFER_TOO_SMALL
+    with pytest.raises(m.MvlmError) as e:
+        dev.gemv_ex(x, F16, W, y, F32, N, K, act=7)
+    assert e.value.code == native.ERR_INVALID_ARG

@@ -235,3 +235,37 @@ def test_batched_against_per_head_products(orc):
         k = Kt.reshape(S, H, D)[:, h, :].copy()
         ref = orc.gemm_nk("f16", q, k, S, S, D)
         assert np.array_equal(C.reshape(H, S, S)[h], ref)
+
+
+# ---- fused epilogue (activations.cl formulas) ------------------------------
+
+def test_gelu_tanh_pins(orc):
+    from scipy.special import erf
+    g = orc.lib().orc_gelu_tanh
+    xs = np.linspace(-6.0, 6.0, 1201)
+    vals = np.array([g(float(x)) for x in xs])
+    assert g(0.0) == 0.0
+    # the tanh form is exactly x-odd-symmetric: gelu(x) - gelu(-x) = x
+    assert np.allclose(vals - vals[::-1], xs, rtol=0, atol=1e-12)
+    # within the tanh approximation's known distance of the erf GELU
+    # (a dropped cubic term or a wrong sqrt(2/pi) would exceed 1e-3)
+    exact = 0.5 * xs * (1.0 + erf(xs / np.sqrt(2.0)))
+    assert np.max(np.abs(vals - exact)) < 1e-3
+    assert abs(g(20.0) - 20.0) < 1e-12 and abs(g(-20.0)) < 1e-12
+
+
+def test_silu_pins(orc):
+    s = orc.lib().orc_silu
+    assert s(0.0) == 0.0
+    for x in (0.1, 1.0, 3.7, 15.0):
+        assert abs((s(x) - s(-x)) - x) < 1e-12          # x sigma(x) + x sigma(-x) = x
+    assert abs(s(np.log(3.0)) - 0.75 * np.log(3.0)) < 1e-15
+
+
+def test_epilogue_order(orc):
+    # act(acc + bias) * mul + res, bias per column, mul/res per element
+    Y = np.array([[1.0, -2.0, 0.0]])
+    out = orc.epilogue_f64(Y, bias=[0.5, 2.0, -1.0], mul=[[2.0, 3.0, 4.0]], res=[[10.0, 20.0, 30.0]], act=2)
+    sil = orc.lib().orc_silu
+    assert np.allclose(out, [[sil(1.5) * 2 + 10, sil(0.0) * 3 + 20, sil(-1.0) * 4 + 30]], rtol=0, atol=1e-15)
+    assert np.array_equal(orc.epilogue_f64(Y), Y)
