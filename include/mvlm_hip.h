@@ -222,6 +222,31 @@ int mvlm_gemm_batched(mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer*
                       int64_t lda, int64_t ldb, int64_t ldc,
                       int64_t strideA, int64_t strideB, int64_t strideC, mvlm_event** ev);
 
+/* ---- fused attention (QK^T -> softmax -> PV in one kernel) ---------------
+ * Q [seq_q][num_heads][head_dim], K and V [seq_kv][num_heads][head_dim], all
+ * fp16 (the layout of attention.cl:44); O [seq_q][num_heads][head_dim] in
+ * o_dtype (F16 or F32).  O = softmax(scale * Q K^T + mask) V per head, with
+ * scale = 1/sqrt(head_dim) when scale == 0.  causal != 0 hides key k from
+ * query q when k > q + (seq_kv - seq_q): queries are the last seq_q positions
+ * of the keys (seq_q <= seq_kv required).  head_dim: a multiple of 8, at most
+ * 128.  Scores and the softmax stay on chip (the 16 x 729 x 729 score tensor
+ * of a SigLIP layer never reaches HBM). */
+int mvlm_attention(mvlm_device* dev, const mvlm_buffer* Q, const mvlm_buffer* K,
+                   const mvlm_buffer* V, mvlm_buffer* O, int o_dtype, int seq_q, int seq_kv,
+                   int num_heads, int head_dim, int causal, float scale, mvlm_event** ev);
+/* Replaces dispatch_attention_prefill (src/engine/compute.h:65,
+ * compute.cpp:305-335; kernel attention.cl:46-179): causal attention of
+ * seq_len queries over seq_len keys, scale 1/sqrt(head_dim), fp16 output. */
+int mvlm_attention_prefill(mvlm_device* dev, const mvlm_buffer* Q, const mvlm_buffer* K,
+                           const mvlm_buffer* V, mvlm_buffer* output, int seq_len, int num_heads,
+                           int head_dim, mvlm_event** ev);
+/* Replaces dispatch_attention_decode (src/engine/compute.h:70,
+ * compute.cpp:337-367; kernel attention.cl:197-295): one query per head
+ * ([1][num_heads][head_dim]) over cache_len cached keys, no mask, fp16 output. */
+int mvlm_attention_decode(mvlm_device* dev, const mvlm_buffer* Q, const mvlm_buffer* K_cache,
+                          const mvlm_buffer* V_cache, mvlm_buffer* output, int cache_len,
+                          int num_heads, int head_dim, mvlm_event** ev);
+
 /* ---- synthetic inputs on the device ------------------------------------- */
 /* SplitMix64 -> Box-Muller fills (same generator as the CPU oracle, computed
  * on the GPU so multi-GB weight sets need no host staging). */
@@ -266,6 +291,9 @@ int mvlm_plan_add_gemm_batched(mvlm_plan* plan, const mvlm_buffer* A, const mvlm
                                mvlm_buffer* C, int batch, int M, int N, int K,
                                int64_t lda, int64_t ldb, int64_t ldc,
                                int64_t strideA, int64_t strideB, int64_t strideC);
+int mvlm_plan_add_attention(mvlm_plan* plan, const mvlm_buffer* Q, const mvlm_buffer* K,
+                            const mvlm_buffer* V, mvlm_buffer* O, int o_dtype, int seq_q, int seq_kv,
+                            int num_heads, int head_dim, int causal, float scale);
 /* enable != 0: capture the plan into a HIP graph (now) and replay it on run. */
 int mvlm_plan_use_graph(mvlm_plan* plan, int enable);
 /* Enqueue the plan `repeats` times; `ev` (optional) spans everything enqueued. */

@@ -1,0 +1,365 @@
+// Fused multi-head attention on CDNA4 matrix cores:
+//   O[q][h][:] = sum_k softmax_k(scale * Q[q][h][:] . K[k][h][:] + mask) V[k][h][:]
+// Q, K, V fp16 [seq][heads][head_dim] (the layout of src/kernels/attention.cl:44-56),
+// fp32 scores and softmax, O fp16 or fp32.
+//
+// Replaces attention_prefill (src/kernels/attention.cl:46-179) and
+// attention_decode (:197-295), which give one (query, head) pair a workgroup
+// and recompute every Q.K dot product three times (max pass, sum pass,
+// weighted-V pass), and the QK^T / softmax / PV round trips through HBM of an
+// unfused version (the 16 x 729 x 729 fp32 score tensor of a SigLIP layer is
+// 34 MB).  Scores never leave registers:
+//  * a block owns 32 queries of one head; its NW waves split the keys
+//    (wave w takes key tiles w, w + NW, ... of 32 keys) and each keeps an
+//    online softmax (running max and sum, rescaled output accumulator); the
+//    block merges the NW partial results through LDS at the end;
+//  * S^T = K Q^T per tile: v_mfma_f32_32x32x16_f16 with A = the K tile (from
+//    the wave's LDS) and B = Q (registers for the whole kernel); lane l's
+//    accumulator column is query l%32 and register r is key
+//    8(r/4) + 4(l/32) + r%4, so a query's softmax statistics are per lane
+//    (plus one exchange with lane l^32);
+//  * O^T = V^T P^T: A = V^T (the V tile stored transposed in LDS), B = the
+//    lane's own probabilities packed to fp16: register r's key order above is
+//    taken as the k order of the product, so A reads V^T columns
+//    {4h..4h+3, 8+4h..8+4h+3} (+16 per k-step) to match, and no data moves
+//    between lanes;
+//  * the output accumulator O^T also has query l%32 per lane, so the online
+//    rescaling is one multiply per register;
+//  * every wave stages its own tiles (no block barrier in the key loop) and
+//    loads tile j+1 into registers while it computes tile j.
+// head_dim is padded to 16 KS (S^T k-steps) and 32 DT (O^T row tiles); the K
+// tile's padding columns are zeroed once, V^T padding rows only feed output
+// rows that are never stored.  Keys past the end are read from the last row
+// (finite data) and get score -inf.  Causal masking hides key k from query q
+// when k > q + (seq_kv - seq_q) (queries aligned to the end of the keys;
+// seq_q == seq_kv gives attention.cl's k > q) and skips the key tiles past
+// the block's last query.
+#include "common.h"
+#include "device_math.h"
+
+#include <algorithm>
+
+namespace mvlm {
+
+struct AttnArgs {
+    const uint16_t* Q;
+    const uint16_t* K;
+    const uint16_t* V;
+    void* O;
+    int o_dtype;
+    int seq_q, seq_kv, heads, D;
+    int causal;
+    float scale_log2;      // scale * log2(e): scores are kept in the exp2 domain
+};
+
+template <int KS, int DT>
+struct AttnLayout {
+    static constexpr int KROW = 16 * KS + 8;                  // K tile row pitch (halfs): odd multiple of 16 B
+    static constexpr int VROW = 36;                           // V^T row pitch (halfs): conflict-free b64 reads
+    static constexpr int STAGE = 32 * KROW * 2 + 32 * DT * VROW * 2;
+    static constexpr int OPITCH = 32 * DT + 4;                // merge area row pitch (floats)
+    static constexpr int MERGE = 32 * OPITCH * 4 + 2 * 32 * 4;
+    static constexpr int REGION = ((STAGE > MERGE ? STAGE : MERGE) + 15) / 16 * 16;   // bytes per wave
+    static constexpr int VI = (32 * DT + 63) / 64;            // quad-chunk rounds per tile (D <= 32 DT)
+};
+
+constexpr int ATTN_LDS_MAX = 160 * 1024;
+
+__device__ __forceinline__ f32x16 mfma_f16(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                  0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+    return (uint32_t)__half_as_ushort(__float2half(lo)) | ((uint32_t)__half_as_ushort(__float2half(hi)) << 16);
+}
+
+// One tile of K and V in registers: lane chunk c = lane + 64 i (i < VI, c < D)
+// covers keys 4 (c % 8) .. +3 and dims 8 (c / 8) .. +7.
+template <int VI>
+struct TileRegs {
+    u32x4 k[VI][4];
+    u32x4 v[VI][4];
+};
+
+template <int KS, int DT, int NW>
+__global__ __launch_bounds__(64 * NW) void attention_kernel(const AttnArgs a) {
+    using L = AttnLayout<KS, DT>;
+    constexpr int VI = L::VI;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int head = blockIdx.y;
+    const int qb0 = blockIdx.x * 32;                      // block's first query
+    const int q = qb0 + l32;                              // this lane's query
+    const int D = a.D;
+    const int64_t row = (int64_t)a.heads * D;             // elements between consecutive positions
+
+    uint8_t* region = lds + wave * L::REGION;
+    uint16_t* ks = (uint16_t*)region;                     // [32 keys][KROW]
+    uint16_t* vt = (uint16_t*)(region + 32 * L::KROW * 2);   // [32 DT dims][VROW]
+
+    // zero the K tile's padding columns D .. 16 KS once (contracted with Q's zeros)
+    for (int i = lane; i < 32 * (16 * KS - D); i += 64) {
+        const int key = i / (16 * KS - D), d = D + i % (16 * KS - D);
+        ks[key * L::KROW + d] = 0;
+    }
+
+    // Q fragments of this lane: Q[q][head][16 s + 8 h .. +7], zero past D / seq_q
+    u32x4 qf[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        const int d = 16 * s + 8 * h;
+        if (q < a.seq_q && d < D) qf[s] = *reinterpret_cast<const u32x4*>(a.Q + (int64_t)q * row + head * D + d);
+        else qf[s] = u32x4{0u, 0u, 0u, 0u};
+    }
+
+    const int shift = a.seq_kv - a.seq_q;
+    const int last_key = a.causal ? min(a.seq_kv - 1, q + shift) : a.seq_kv - 1;   // lane's last visible key
+    int kv_end = a.seq_kv;
+    if (a.causal) kv_end = min(a.seq_kv, min(qb0 + 32, a.seq_q) + shift);
+
+    const uint16_t* kbase = a.K + head * D;
+    const uint16_t* vbase = a.V + head * D;
+    TileRegs<VI> tr;
+    auto load_tile = [&](int kv0) {
+#pragma unroll
+        for (int i = 0; i < VI; ++i) {
+            const int c = lane + 64 * i;
+            if (c < D) {
+                const int d = 8 * (c >> 3);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int key = min(kv0 + 4 * (c & 7) + u, a.seq_kv - 1);
+                    tr.k[i][u] = *reinterpret_cast<const u32x4*>(kbase + (int64_t)key * row + d);
+                    tr.v[i][u] = *reinterpret_cast<const u32x4*>(vbase + (int64_t)key * row + d);
+                }
+            }
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int i = 0; i < VI; ++i) {
+            const int c = lane + 64 * i;
+            if (c < D) {
+                const int key0 = 4 * (c & 7), d = 8 * (c >> 3);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) *reinterpret_cast<u32x4*>(ks + (key0 + u) * L::KROW + d) = tr.k[i][u];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    // dim d + j of keys key0 .. key0+3
+                    const int sh = 16 * (j & 1);
+                    const uint32_t k01 = ((tr.v[i][0][j >> 1] >> sh) & 0xFFFFu) | (((tr.v[i][1][j >> 1] >> sh) & 0xFFFFu) << 16);
+                    const uint32_t k23 = ((tr.v[i][2][j >> 1] >> sh) & 0xFFFFu) | (((tr.v[i][3][j >> 1] >> sh) & 0xFFFFu) << 16);
+                    *reinterpret_cast<u32x2*>(vt + (d + j) * L::VROW + key0) = u32x2{k01, k23};
+                }
+            }
+        }
+    };
+
+    float mrun = -INFINITY, lrun = 0.0f;
+    f32x16 oacc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[t][r] = 0.0f;
+
+    int kv0 = 32 * wave;
+    if (kv0 < kv_end) load_tile(kv0);
+    while (kv0 < kv_end) {
+        store_tile();
+        const int kv_next = kv0 + 32 * NW;
+        if (kv_next < kv_end) load_tile(kv_next);      // in flight while this tile computes
+        // this wave's own LDS: its stores above precede these reads in the wave's LDS order
+        asm volatile("" ::: "memory");
+
+        f32x16 s;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+#pragma unroll
+        for (int st = 0; st < KS; ++st) {
+            const u32x4 kf = *reinterpret_cast<const u32x4*>(ks + l32 * L::KROW + 16 * st + 8 * h);
+            s = mfma_f16(kf, qf[st], s);
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = kv0 + 8 * (r >> 2) + 4 * h + (r & 3);
+            s[r] = key > last_key ? -INFINITY : s[r] * a.scale_log2;
+            tmax = fmaxf(tmax, s[r]);
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mnew = fmaxf(mrun, tmax);
+        // mnew stays -inf while every key so far is hidden from this query
+        const float msafe = mnew == -INFINITY ? 0.0f : mnew;
+        const float factor = __builtin_amdgcn_exp2f(mrun - msafe);
+        float psum = 0.0f;
+        float p[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            p[r] = __builtin_amdgcn_exp2f(s[r] - msafe);
+            psum += p[r];
+        }
+        psum += __shfl_xor(psum, 32, 64);
+        lrun = lrun * factor + psum;
+        mrun = mnew;
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[t][r] *= factor;
+
+        // O^T += V^T P^T over the tile's two 16-key steps
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            u32x4 pb;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) pb[j] = pack_f16x2(p[8 * kk + 2 * j], p[8 * kk + 2 * j + 1]);
+#pragma unroll
+            for (int t = 0; t < DT; ++t) {
+                const uint16_t* vrow = vt + (32 * t + l32) * L::VROW + 16 * kk + 4 * h;
+                const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
+                const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
+                oacc[t] = mfma_f16(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb, oacc[t]);
+            }
+        }
+        asm volatile("" ::: "memory");                  // the next tile's stores follow these reads
+        kv0 = kv_next;
+    }
+
+    auto store4 = [&](int qq, int d, float v0, float v1, float v2, float v3) {
+        const int64_t off = (int64_t)qq * row + head * D + d;
+        if (a.o_dtype == MVLM_F32)
+            *reinterpret_cast<f32x4*>((float*)a.O + off) = f32x4{v0, v1, v2, v3};
+        else
+            *reinterpret_cast<u32x2*>((uint16_t*)a.O + off) = u32x2{pack_f16x2(v0, v1), pack_f16x2(v2, v3)};
+    };
+
+    if constexpr (NW == 1) {
+        if (q >= a.seq_q) return;
+        const float inv = 1.0f / lrun;
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = 32 * t + 8 * g + 4 * h;      // registers 4g .. 4g+3: dims d .. d+3
+                if (d < D)
+                    store4(q, d, oacc[t][4 * g] * inv, oacc[t][4 * g + 1] * inv, oacc[t][4 * g + 2] * inv,
+                           oacc[t][4 * g + 3] * inv);
+            }
+    } else {
+        // merge the NW partial softmaxes: each wave parks (m, l, unnormalized O)
+        // in its own region, then the block combines them per (query, 4 dims)
+        float* om = (float*)region;                       // [32 queries][OPITCH]
+        float* ml = om + 32 * L::OPITCH;                  // m[32], l[32]
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = 32 * t + 8 * g + 4 * h;
+                *reinterpret_cast<f32x4*>(om + l32 * L::OPITCH + d) =
+                    f32x4{oacc[t][4 * g], oacc[t][4 * g + 1], oacc[t][4 * g + 2], oacc[t][4 * g + 3]};
+            }
+        if (h == 0) {
+            ml[l32] = mrun;
+            ml[32 + l32] = lrun;
+        }
+        __syncthreads();
+        for (int it = threadIdx.x; it < 32 * (D / 4); it += 64 * NW) {
+            const int ql = it & 31, d = 4 * (it >> 5);
+            if (qb0 + ql >= a.seq_q) continue;
+            float mw[NW], mx = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                mw[w] = ((const float*)(lds + w * L::REGION))[32 * L::OPITCH + ql];
+                mx = fmaxf(mx, mw[w]);
+            }
+            float lsum = 0.0f;
+            f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                const float* rw = (const float*)(lds + w * L::REGION);
+                const float f = __builtin_amdgcn_exp2f(mw[w] - mx);
+                lsum += f * rw[32 * L::OPITCH + 32 + ql];
+                o += f * *reinterpret_cast<const f32x4*>(rw + ql * L::OPITCH + d);
+            }
+            const float inv = 1.0f / lsum;
+            store4(qb0 + ql, d, o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
+        }
+    }
+}
+
+template <int KS, int DT, int NW>
+static hipError_t launch_variant(hipStream_t s, const AttnArgs& a) {
+    auto kernel = attention_kernel<KS, DT, NW>;
+    constexpr int lds = NW * AttnLayout<KS, DT>::REGION;
+    static_assert(lds <= ATTN_LDS_MAX, "attention LDS over budget");
+    static bool attr_set = false;
+    if (!attr_set) {
+        const hipError_t e =
+            hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, ATTN_LDS_MAX);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const dim3 grid((unsigned)((a.seq_q + 31) / 32), (unsigned)a.heads);
+    launch_kernel(kernel, grid, dim3(64 * NW), (uint32_t)lds, s, a);
+    return hipGetLastError();
+}
+
+// Waves per block: the fewest block rounds times key tiles per wave, with
+// blocks per CU bounded by LDS and by the resident waves the register use
+// allows (about 3 per SIMD up to 64 dims, 2 up to 96, 1 beyond); ties go to
+// fewer waves.
+template <int KS, int DT>
+static int pick_waves(int blocks, int key_tiles, int num_cus) {
+    constexpr int region = AttnLayout<KS, DT>::REGION;
+    constexpr int waves_per_cu = DT <= 2 ? 12 : DT == 3 ? 8 : 4;
+    int best = 1;
+    int64_t best_cost = INT64_MAX;
+    for (int nw = 1; nw <= 16; nw *= 2) {
+        if (nw * region > ATTN_LDS_MAX) break;
+        const int per_cu = std::max(1, std::min(ATTN_LDS_MAX / (nw * region), waves_per_cu / nw));
+        const int64_t rounds = (blocks + (int64_t)num_cus * per_cu - 1) / ((int64_t)num_cus * per_cu);
+        const int64_t cost = rounds * ((key_tiles + nw - 1) / nw);
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = nw;
+        }
+    }
+    return best;
+}
+
+template <int KS, int DT>
+static hipError_t launch_dims(hipStream_t s, const AttnArgs& a, int num_cus) {
+    const int blocks = (a.seq_q + 31) / 32 * a.heads;
+    const int nw = pick_waves<KS, DT>(blocks, (a.seq_kv + 31) / 32, num_cus);
+    switch (nw) {
+        case 1: return launch_variant<KS, DT, 1>(s, a);
+        case 2: return launch_variant<KS, DT, 2>(s, a);
+        case 4: return launch_variant<KS, DT, 4>(s, a);
+        case 8: return launch_variant<KS, DT, 8>(s, a);
+        default:
+            if constexpr (16 * AttnLayout<KS, DT>::REGION <= ATTN_LDS_MAX) return launch_variant<KS, DT, 16>(s, a);
+            return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_attention(hipStream_t s, const void* Q, const void* K, const void* V, void* O, int o_dtype,
+                            int seq_q, int seq_kv, int heads, int head_dim, int causal, float scale, int num_cus) {
+    AttnArgs a{};
+    a.Q = (const uint16_t*)Q; a.K = (const uint16_t*)K; a.V = (const uint16_t*)V; a.O = O;
+    a.o_dtype = o_dtype;
+    a.seq_q = seq_q; a.seq_kv = seq_kv; a.heads = heads; a.D = head_dim;
+    a.causal = causal;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    if (head_dim <= 32) return launch_dims<2, 1>(s, a, num_cus);
+    if (head_dim <= 48) return launch_dims<3, 2>(s, a, num_cus);
+    if (head_dim <= 64) return launch_dims<4, 2>(s, a, num_cus);
+    if (head_dim <= 80) return launch_dims<5, 3>(s, a, num_cus);
+    if (head_dim <= 96) return launch_dims<6, 3>(s, a, num_cus);
+    if (head_dim <= 112) return launch_dims<7, 4>(s, a, num_cus);
+    if (head_dim <= 128) return launch_dims<8, 4>(s, a, num_cus);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace mvlm

@@ -155,6 +155,9 @@ hipError_t launch_gemm_mfma(hipStream_t s, const void* A, int ab_dtype, const vo
                             int c_dtype, int batch, int M, int N, int K, int64_t lda, int64_t ldb,
                             int64_t ldc, int64_t strideA, int64_t strideB, int64_t strideC,
                             int kread_b, int num_cus, const Epilogue* ep = nullptr);
+// fused attention, fp16 Q/K/V [seq][heads][head_dim], head_dim a multiple of 8 up to 128
+hipError_t launch_attention(hipStream_t s, const void* Q, const void* K, const void* V, void* O, int o_dtype,
+                            int seq_q, int seq_kv, int heads, int head_dim, int causal, float scale, int num_cus);
 hipError_t launch_pack(hipStream_t s, const void* src, int dtype, int layout, int N, int K,
                        mvlm_weight* w);
 hipError_t launch_dequant(hipStream_t s, const mvlm_weight* w, float* out);

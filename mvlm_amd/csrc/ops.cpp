@@ -8,6 +8,7 @@
 // replaying a captured HIP graph.
 #include "common.h"
 
+#include <cmath>
 #include <new>
 #include <vector>
 
@@ -15,12 +16,13 @@ using namespace mvlm;
 
 namespace {
 
-enum OpKind { OP_GEMM_NAIVE, OP_GEMM_TILED, OP_GEMM_MFMA, OP_GEMV_DENSE, OP_GEMV_QUANT, OP_GEMV_GROUP };
+enum OpKind { OP_GEMM_NAIVE, OP_GEMM_TILED, OP_GEMM_MFMA, OP_GEMV_DENSE, OP_GEMV_QUANT, OP_GEMV_GROUP, OP_ATTENTION };
 
 struct Op {
     OpKind kind;
     const void* a = nullptr;      // A / x / X
-    const void* b = nullptr;      // B (naive, tiled, batched)
+    const void* b = nullptr;      // B (naive, tiled, batched); K (attention)
+    const void* v = nullptr;      // V (attention)
     void* c = nullptr;            // C / y / Y
     const mvlm_weight* w = nullptr;
     int a_dtype = MVLM_F16, c_dtype = MVLM_F32;
@@ -35,6 +37,9 @@ struct Op {
     void* gy[MVLM_MAX_GROUP] = {};
     int gyd[MVLM_MAX_GROUP] = {};
     Epilogue ep;                  // fused epilogue (GEMM MFMA, GEMV)
+    // attention: M = seq_q, N = seq_kv, batch = heads, K = head_dim
+    int causal = 0;
+    float scale = 0.0f;
 };
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -141,6 +146,40 @@ int make_gemm_batched(mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer*
     return MVLM_OK;
 }
 
+int make_attention(mvlm_device* dev, const mvlm_buffer* Q, const mvlm_buffer* K, const mvlm_buffer* V,
+                   mvlm_buffer* O, int o_dtype, int seq_q, int seq_kv, int heads, int head_dim, int causal,
+                   float scale, const char* fn, Op* op) {
+    REQUIRE(dev && Q && K && V && O, "%s: null argument", fn);
+    REQUIRE(Q->dev == dev && K->dev == dev && V->dev == dev && O->dev == dev, "%s: buffers belong to another device",
+            fn);
+    REQUIRE(seq_q > 0 && seq_kv > 0 && heads > 0 && head_dim > 0,
+            "%s: seq_q=%d seq_kv=%d num_heads=%d head_dim=%d must be positive", fn, seq_q, seq_kv, heads, head_dim);
+    REQUIRE(o_dtype == MVLM_F16 || o_dtype == MVLM_F32, "%s: output dtype %d is not F16/F32", fn, o_dtype);
+    REQUIRE(!causal || seq_q <= seq_kv, "%s: causal attention needs seq_q (%d) <= seq_kv (%d)", fn, seq_q, seq_kv);
+    REQUIRE(scale >= 0.0f && scale < INFINITY, "%s: scale %g must be finite and non-negative", fn, (double)scale);
+    if (head_dim % 8 != 0 || head_dim > 128)
+        return set_error(MVLM_ERR_UNSUPPORTED, "%s: head_dim=%d must be a multiple of 8 and at most 128", fn,
+                         head_dim);
+    REQUIRE(heads <= 65535 && (int64_t)heads * head_dim <= (1 << 24) && (int64_t)seq_q * heads <= (1 << 30) &&
+                (int64_t)seq_kv * heads <= (1 << 30),
+            "%s: shape too large", fn);
+    REQUIRE(aligned16(Q->ptr) && aligned16(K->ptr) && aligned16(V->ptr) && aligned16(O->ptr),
+            "%s: Q, K, V and O must be 16-byte aligned", fn);
+    const size_t row = (size_t)heads * head_dim;
+    NEED(Q, (size_t)seq_q * row * 2, "Q");
+    NEED(K, (size_t)seq_kv * row * 2, "K");
+    NEED(V, (size_t)seq_kv * row * 2, "V");
+    NEED(O, (size_t)seq_q * row * dtype_size(o_dtype), "O");
+    op->kind = OP_ATTENTION;
+    op->a = Q->ptr; op->b = K->ptr; op->v = V->ptr; op->c = O->ptr;
+    op->c_dtype = o_dtype;
+    op->M = seq_q; op->N = seq_kv; op->batch = heads; op->K = head_dim;
+    op->causal = causal ? 1 : 0;
+    op->scale = scale == 0.0f ? 1.0f / sqrtf((float)head_dim) : scale;
+    op->num_cus = dev->prop.multiProcessorCount;
+    return MVLM_OK;
+}
+
 // Dense GEMV (M == 1) or dequantizing GEMV / skinny GEMM (M <= 16).
 // want_dtype: required weight dtype, or -1 for any.
 int make_gemv(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W, mvlm_buffer* y,
@@ -219,6 +258,9 @@ hipError_t enqueue_op(hipStream_t s, const Op& op) {
                 return launch_gemv_stream(s, op.a, MVLM_F32, op.w, op.c, MVLM_F32, op.num_cus, &op.ep);
             return launch_gemm_skinny(s, (const float*)op.a, op.w, (float*)op.c, op.M, op.N, op.K, op.num_cus,
                                       &op.ep);
+        case OP_ATTENTION:
+            return launch_attention(s, op.a, op.b, op.v, op.c, op.c_dtype, op.M, op.N, op.batch, op.K, op.causal,
+                                    op.scale, op.num_cus);
     }
     return hipErrorInvalidValue;
 }
@@ -327,6 +369,28 @@ extern "C" int mvlm_gemm_q4_0(mvlm_device* dev, const mvlm_buffer* X, const mvlm
     RUN(make_gemv(dev, X, MVLM_F32, W, Y, MVLM_F32, M, N, K, MVLM_Q4_0, fn, &op));
 }
 
+extern "C" int mvlm_attention(mvlm_device* dev, const mvlm_buffer* Q, const mvlm_buffer* K, const mvlm_buffer* V,
+                              mvlm_buffer* O, int o_dtype, int seq_q, int seq_kv, int num_heads, int head_dim,
+                              int causal, float scale, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(make_attention(dev, Q, K, V, O, o_dtype, seq_q, seq_kv, num_heads, head_dim, causal, scale, fn, &op));
+}
+
+extern "C" int mvlm_attention_prefill(mvlm_device* dev, const mvlm_buffer* Q, const mvlm_buffer* K,
+                                      const mvlm_buffer* V, mvlm_buffer* output, int seq_len, int num_heads,
+                                      int head_dim, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(make_attention(dev, Q, K, V, output, MVLM_F16, seq_len, seq_len, num_heads, head_dim, 1, 0.0f, fn, &op));
+}
+
+extern "C" int mvlm_attention_decode(mvlm_device* dev, const mvlm_buffer* Q, const mvlm_buffer* K_cache,
+                                     const mvlm_buffer* V_cache, mvlm_buffer* output, int cache_len, int num_heads,
+                                     int head_dim, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(make_attention(dev, Q, K_cache, V_cache, output, MVLM_F16, 1, cache_len, num_heads, head_dim, 0, 0.0f, fn,
+                       &op));
+}
+
 // ---------------------------------------------------------------------------
 // plans
 // ---------------------------------------------------------------------------
@@ -429,6 +493,17 @@ extern "C" int mvlm_plan_add_gemm_batched(mvlm_plan* plan, const mvlm_buffer* A,
     REQUIRE(plan, "%s: null argument", fn);
     Op op{};
     int st = make_gemm_batched(plan->dev, A, B, C, batch, M, N, K, lda, ldb, ldc, strideA, strideB, strideC, fn, &op);
+    return st != MVLM_OK ? st : plan_push(plan, op);
+}
+
+extern "C" int mvlm_plan_add_attention(mvlm_plan* plan, const mvlm_buffer* Q, const mvlm_buffer* K,
+                                       const mvlm_buffer* V, mvlm_buffer* O, int o_dtype, int seq_q, int seq_kv,
+                                       int num_heads, int head_dim, int causal, float scale) {
+    const char* fn = __func__;
+    REQUIRE(plan, "%s: null argument", fn);
+    Op op{};
+    int st = make_attention(plan->dev, Q, K, V, O, o_dtype, seq_q, seq_kv, num_heads, head_dim, causal, scale, fn,
+                            &op);
     return st != MVLM_OK ? st : plan_push(plan, op);
 }
 

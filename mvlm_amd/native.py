@@ -112,6 +112,10 @@ _SIGNATURES = {
     "mvlm_gemm_q4_0": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _PP]),
     "mvlm_gemm_batched": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int,
                                   c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, _PP]),
+    "mvlm_attention": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, _PP]),
+    "mvlm_attention_prefill": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, _PP]),
+    "mvlm_attention_decode": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, _PP]),
+    "mvlm_plan_add_attention": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_float]),
     "mvlm_fill_normal": (c_int, [_P, _P, c_int, c_size_t, c_uint64, c_double]),
     "mvlm_weight_random": (c_int, [_P, c_int, c_int, c_int, c_uint64, c_double, _PP]),
     "mvlm_event_wait": (c_int, [_P]),
@@ -422,6 +426,12 @@ class Plan:
         self._keep += [A, B, C]
         return self
 
+    def add_attention(self, Q, K, V, O, o_dtype, seq_q, seq_kv, num_heads, head_dim, causal=False, scale=0.0):
+        _call("mvlm_plan_add_attention", self.handle, Q.handle, K.handle, V.handle, O.handle, o_dtype, seq_q,
+              seq_kv, num_heads, head_dim, 1 if causal else 0, scale)
+        self._keep += [Q, K, V, O]
+        return self
+
     def use_graph(self, enable=True):
         _call("mvlm_plan_use_graph", self.handle, 1 if enable else 0)
         return self
@@ -561,6 +571,20 @@ class Device:
     def gemm_batched(self, A, B, C, batch, M, N, K, lda, ldb, ldc, sA, sB, sC, event=False):
         return self._launch("mvlm_gemm_batched", (A.handle, B.handle, C.handle, batch, M, N, K,
                                                   lda, ldb, ldc, sA, sB, sC), event)
+
+    def attention(self, Q, K, V, O, o_dtype, seq_q, seq_kv, num_heads, head_dim, causal=False, scale=0.0,
+                  event=False):
+        """O = softmax(scale Q K^T + mask) V per head; [seq][heads][head_dim] fp16 in, F16/F32 out."""
+        return self._launch("mvlm_attention", (Q.handle, K.handle, V.handle, O.handle, o_dtype, seq_q, seq_kv,
+                                               num_heads, head_dim, 1 if causal else 0, scale), event)
+
+    def attention_prefill(self, Q, K, V, O, seq_len, num_heads, head_dim, event=False):
+        return self._launch("mvlm_attention_prefill", (Q.handle, K.handle, V.handle, O.handle, seq_len, num_heads,
+                                                       head_dim), event)
+
+    def attention_decode(self, Q, K_cache, V_cache, O, cache_len, num_heads, head_dim, event=False):
+        return self._launch("mvlm_attention_decode", (Q.handle, K_cache.handle, V_cache.handle, O.handle, cache_len,
+                                                      num_heads, head_dim), event)
 
     def gemm_quant(self, X, W, Y, M, N, K, event=False):
         """Dispatch by the weight's dtype (Q8_0 or Q4_0)."""

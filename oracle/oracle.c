@@ -475,3 +475,56 @@ void orc_epilogue_f64(double* Y, const double* bias, const double* mul, const do
             Y[i] = v;
         }
 }
+
+void orc_attention_f64(const uint16_t* Q, const uint16_t* K, const uint16_t* V, double* O, double* A, double* R,
+                       int seq_q, int seq_kv, int heads, int D, int causal, double scale, int nthreads) {
+    const int nt = clamp_threads(nthreads);
+    const size_t row = (size_t)heads * D;
+    const int shift = seq_kv - seq_q;
+    #pragma omp parallel num_threads(nt)
+    {
+        double* s = (double*)malloc(sizeof(double) * (size_t)(seq_kv > 0 ? seq_kv : 1));
+        double* q = (double*)malloc(sizeof(double) * (size_t)D);
+        #pragma omp for schedule(dynamic, 4)
+        for (long qh = 0; qh < (long)seq_q * heads; ++qh) {
+            const int qi = (int)(qh / heads), h = (int)(qh % heads);
+            const uint16_t* qp = Q + (size_t)qi * row + (size_t)h * D;
+            for (int d = 0; d < D; ++d) q[d] = H2F(qp[d]);
+            int last = seq_kv - 1;
+            if (causal && qi + shift < last) last = qi + shift;
+            double m = -INFINITY, r = 0.0;
+            for (int k = 0; k <= last; ++k) {
+                const uint16_t* kp = K + (size_t)k * row + (size_t)h * D;
+                double acc = 0.0, mag = 0.0;
+                for (int d = 0; d < D; ++d) {
+                    const double pr = q[d] * H2F(kp[d]);
+                    acc += pr;
+                    mag += fabs(pr);
+                }
+                s[k] = scale * acc;
+                if (s[k] > m) m = s[k];
+                if (scale * mag > r) r = scale * mag;
+            }
+            double l = 0.0;
+            for (int k = 0; k <= last; ++k) {
+                s[k] = exp(s[k] - m);
+                l += s[k];
+            }
+            double* o = O + (size_t)qi * row + (size_t)h * D;
+            double* a = A + (size_t)qi * row + (size_t)h * D;
+            for (int d = 0; d < D; ++d) o[d] = a[d] = 0.0;
+            for (int k = 0; k <= last; ++k) {
+                const uint16_t* vp = V + (size_t)k * row + (size_t)h * D;
+                const double w = s[k] / l;
+                for (int d = 0; d < D; ++d) {
+                    const double v = H2F(vp[d]);
+                    o[d] += w * v;
+                    a[d] += w * fabs(v);
+                }
+            }
+            R[qh] = r;
+        }
+        free(s);
+        free(q);
+    }
+}

@@ -22,6 +22,8 @@
  *                    ascending k, weights stored [N,K] as in GGUF.
  *   orc_*_f64        fp64 brute force plus the scale sum_k |a_k * b_k| used by the
  *                    tolerance |y - r| <= rtol * scale.
+ *   orc_attention_f64  src/kernels/attention.cl:46-179 / :197-295 (softmax(Q K^T
+ *                    / sqrt(d) + causal mask) V per head) in fp64.
  *
  * Pinning (each function has at least one check that does not retype it):
  * golden fixtures under tests/golden/, closed forms (one-hot, identity,
@@ -107,6 +109,16 @@ void orc_gemm_f64_nk(const double* X, const double* W, double* Y, double* S,
 double orc_gelu_tanh(double x);
 double orc_silu(double x);
 void orc_epilogue_f64(double* Y, const double* bias, const double* mul, const double* res, int act, int M, int N);
+
+/* ---- attention (src/kernels/attention.cl:46-179 prefill, :197-295 decode) --
+ * Q [seq_q][heads][D], K/V [seq_kv][heads][D] fp16 bits; per (query, head):
+ * s_k = scale * sum_d Q[d] K[k][d] (fp64), keys with k > q + (seq_kv - seq_q)
+ * masked when causal (attention.cl:96: kv_pos > query_pos when seq_q ==
+ * seq_kv), p_k = exp(s_k - max) / sum, O[d] = sum_k p_k V[k][d].
+ * Also returns A[q][h][d] = sum_k p_k |V[k][d]| (the error scale of O) and
+ * R[q][h] = max_k scale * sum_d |Q[d] K[k][d]| (the error scale of a score). */
+void orc_attention_f64(const uint16_t* Q, const uint16_t* K, const uint16_t* V, double* O, double* A, double* R,
+                       int seq_q, int seq_kv, int heads, int D, int causal, double scale, int nthreads);
 
 int orc_max_threads(void);
 

@@ -69,6 +69,7 @@ def lib():
                                             ctypes.c_long, ctypes.c_long, ctypes.c_long]),
             "orc_gemm_f64_nk": (None, [_f64p, _f64p, _f64p, _f64p, i, i, i, i]),
             "orc_max_threads": (i, []),
+            "orc_attention_f64": (None, [_u16p, _u16p, _u16p, _f64p, _f64p, _f64p, i, i, i, i, i, d, i]),
             "orc_gelu_tanh": (d, [d]),
             "orc_silu": (d, [d]),
             "orc_epilogue_f64": (None, [_f64p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, i, i, i]),
@@ -232,3 +233,17 @@ def gemm_batched_f16(A, B, batch, M, N, K, lda, ldb, ldc, sA, sB, sC, c_elems):
                                np.ascontiguousarray(B, np.uint16).ravel(), C,
                                batch, M, N, K, lda, ldb, ldc, sA, sB, sC)
     return C
+
+
+def attention_f64(Q, K, V, seq_q, seq_kv, heads, D, causal=False, scale=None, nthreads=0):
+    """fp64 attention of fp16-bit Q/K/V ([seq][heads][D]); returns (O, A, R):
+    O and A = sum_k p_k |V_k| as [seq_q, heads, D], R = max_k scale sum_d |q k| as [seq_q, heads]."""
+    if scale is None:
+        scale = 1.0 / np.sqrt(D)
+    O = np.empty(seq_q * heads * D, np.float64)
+    A = np.empty_like(O)
+    R = np.empty(seq_q * heads, np.float64)
+    lib().orc_attention_f64(np.ascontiguousarray(Q, np.uint16).ravel(), np.ascontiguousarray(K, np.uint16).ravel(),
+                            np.ascontiguousarray(V, np.uint16).ravel(), O, A, R, seq_q, seq_kv, heads, D,
+                            1 if causal else 0, float(scale), nthreads)
+    return O.reshape(seq_q, heads, D), A.reshape(seq_q, heads, D), R.reshape(seq_q, heads)

@@ -269,3 +269,109 @@ def test_epilogue_order(orc):
     sil = orc.lib().orc_silu
     assert np.allclose(out, [[sil(1.5) * 2 + 10, sil(0.0) * 3 + 20, sil(-1.0) * 4 + 30]], rtol=0, atol=1e-15)
     assert np.array_equal(orc.epilogue_f64(Y), Y)
+
+
+# ---- attention (attention.cl:46-179 prefill, :197-295 decode) ----------------
+
+def _f16(x):
+    """fp16 bits of x by numpy's own RNE conversion, and the values they hold."""
+    bits = np.asarray(x, np.float16).view(np.uint16)
+    return bits, bits.view(np.float16).astype(np.float64)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_constant_values(orc, causal):
+    # V constant along the keys: every convex combination returns it
+    rng = np.random.default_rng(11)
+    Sq, Skv, H, D = 7, 13, 3, 16
+    Q, _ = _f16(rng.standard_normal((Sq, H, D)))
+    K, _ = _f16(rng.standard_normal((Skv, H, D)))
+    c = rng.standard_normal((H, D))
+    V, cv = _f16(np.broadcast_to(c, (Skv, H, D)))
+    O, A, _ = orc.attention_f64(Q, K, V, Sq, Skv, H, D, causal)
+    assert np.allclose(O, np.broadcast_to(cv[0], O.shape), rtol=1e-14, atol=0)
+    assert np.allclose(A, np.abs(O), rtol=1e-14, atol=0)
+
+
+def test_attention_zero_query_is_running_mean(orc):
+    # Q = 0: all visible scores equal, so O is the mean of the visible V rows.
+    # Causal with seq_q < seq_kv: query i sees keys 0 .. i + (seq_kv - seq_q).
+    rng = np.random.default_rng(12)
+    Sq, Skv, H, D = 5, 9, 2, 8
+    Q, _ = _f16(np.zeros((Sq, H, D)))
+    K, _ = _f16(rng.standard_normal((Skv, H, D)))
+    V, v = _f16(rng.standard_normal((Skv, H, D)))
+    O, _, _ = orc.attention_f64(Q, K, V, Sq, Skv, H, D, causal=False)
+    assert np.allclose(O, np.broadcast_to(v.mean(axis=0), O.shape), rtol=0, atol=1e-14)
+    O, _, _ = orc.attention_f64(Q, K, V, Sq, Skv, H, D, causal=True)
+    running = np.cumsum(v, axis=0) / np.arange(1, Skv + 1)[:, None, None]
+    assert np.allclose(O, running[Skv - Sq:], rtol=0, atol=1e-14)
+
+
+def test_attention_causal_first_query_is_first_value(orc):
+    rng = np.random.default_rng(13)
+    S, H, D = 6, 4, 24
+    Q, _ = _f16(rng.standard_normal((S, H, D)))
+    K, _ = _f16(rng.standard_normal((S, H, D)))
+    V, v = _f16(rng.standard_normal((S, H, D)))
+    O, _, _ = orc.attention_f64(Q, K, V, S, S, H, D, causal=True)
+    assert np.array_equal(O[0], v[0])
+    # the last query sees every key: same row as the unmasked product
+    O2, _, _ = orc.attention_f64(Q, K, V, S, S, H, D, causal=False)
+    assert np.array_equal(O[-1], O2[-1])
+
+
+def test_attention_two_keys_is_a_sigmoid(orc):
+    # two keys: weights sigma(s0 - s1), sigma(s1 - s0) with s = q.k / sqrt(64) = q.k / 8
+    rng = np.random.default_rng(14)
+    H, D = 3, 64
+    Q, q = _f16(rng.standard_normal((1, H, D)))
+    K, k = _f16(rng.standard_normal((2, H, D)))
+    V, v = _f16(rng.standard_normal((2, H, D)))
+    O, _, R = orc.attention_f64(Q, K, V, 1, 2, H, D)
+    s = np.einsum("hd,khd->kh", q[0], k) / 8.0
+    w0 = 1.0 / (1.0 + np.exp(s[1] - s[0]))
+    want = w0[:, None] * v[0] + (1.0 - w0)[:, None] * v[1]
+    assert np.allclose(O[0], want, rtol=1e-12, atol=1e-14)
+    assert np.allclose(R[0], np.max(np.einsum("hd,khd->khd", q[0], k).__abs__().sum(-1), axis=0) / 8.0,
+                       rtol=1e-14)
+    # an explicit scale replaces 1/sqrt(D)
+    O3, _, _ = orc.attention_f64(Q, K, V, 1, 2, H, D, scale=0.0)
+    assert np.allclose(O3[0], 0.5 * (v[0] + v[1]), rtol=0, atol=1e-15)
+
+
+def test_attention_selects_matching_key(orc):
+    # one-hot keys and queries: query (i, h) matches key (3i + h) % 16 only, with
+    # score 64 / sqrt(16) = 16 against 0, so O is that key's V row to within
+    # 15 e^-16 of its magnitude; a transposed or head-swapped index picks another row
+    H, D, Skv, Sq = 2, 16, 16, 10
+    K = np.zeros((Skv, H, D))
+    for k in range(Skv):
+        for h in range(H):
+            K[k, h, (k + 5 * h) % D] = 8.0
+    Qv = np.zeros((Sq, H, D))
+    match = np.zeros((Sq, H), int)
+    for i in range(Sq):
+        for h in range(H):
+            match[i, h] = (3 * i + h) % Skv
+            Qv[i, h] = K[match[i, h], h]
+    Qb, _ = _f16(Qv)
+    Kb, _ = _f16(K)
+    rng = np.random.default_rng(15)
+    V, v = _f16(rng.uniform(1.0, 2.0, (Skv, H, D)))
+    O, _, _ = orc.attention_f64(Qb, Kb, V, Sq, Skv, H, D)
+    for i in range(Sq):
+        for h in range(H):
+            assert np.allclose(O[i, h], v[match[i, h], h], rtol=15 * np.exp(-16.0) * 2, atol=0), (i, h)
+
+
+def test_attention_heads_are_independent(orc):
+    rng = np.random.default_rng(16)
+    S, H, D = 8, 5, 8
+    Q, _ = _f16(rng.standard_normal((S, H, D)))
+    K, _ = _f16(rng.standard_normal((S, H, D)))
+    V, _ = _f16(rng.standard_normal((S, H, D)))
+    perm = rng.permutation(H)
+    O, _, _ = orc.attention_f64(Q, K, V, S, S, H, D, causal=True)
+    Op, _, _ = orc.attention_f64(Q[:, perm], K[:, perm], V[:, perm], S, S, H, D, causal=True)
+    assert np.array_equal(Op, O[:, perm])
