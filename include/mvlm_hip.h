@@ -247,6 +247,17 @@ int mvlm_attention_decode(mvlm_device* dev, const mvlm_buffer* Q, const mvlm_buf
                           const mvlm_buffer* V_cache, mvlm_buffer* output, int cache_len,
                           int num_heads, int head_dim, mvlm_event** ev);
 
+/* ---- token pick: row-wise argmax on the device ----------------------------
+ * Replaces argmax_logits (src/models/moondream2.cpp:553-593), which reads the
+ * fp16 logits back to the host and scans them.  out_index[r] (int32, device)
+ * = the first index of the largest key of row r of x (rows x n, leading
+ * dimension ld elements, dtype F32/F16/BF16).  Key: zeros and subnormals
+ * count as 0, inf and NaN as +inf or -inf by their sign, other values as
+ * themselves (the reference's fp16 decode, moondream2.cpp:571-583); a row of
+ * -inf returns 0. */
+int mvlm_argmax(mvlm_device* dev, const mvlm_buffer* x, int dtype, int rows, int n, int64_t ld,
+                mvlm_buffer* out_index, mvlm_event** ev);
+
 /* ---- synthetic inputs on the device ------------------------------------- */
 /* SplitMix64 -> Box-Muller fills (same generator as the CPU oracle, computed
  * on the GPU so multi-GB weight sets need no host staging). */
@@ -294,6 +305,8 @@ int mvlm_plan_add_gemm_batched(mvlm_plan* plan, const mvlm_buffer* A, const mvlm
 int mvlm_plan_add_attention(mvlm_plan* plan, const mvlm_buffer* Q, const mvlm_buffer* K,
                             const mvlm_buffer* V, mvlm_buffer* O, int o_dtype, int seq_q, int seq_kv,
                             int num_heads, int head_dim, int causal, float scale);
+int mvlm_plan_add_argmax(mvlm_plan* plan, const mvlm_buffer* x, int dtype, int rows, int n, int64_t ld,
+                         mvlm_buffer* out_index);
 /* enable != 0: capture the plan into a HIP graph (now) and replay it on run. */
 int mvlm_plan_use_graph(mvlm_plan* plan, int enable);
 /* Enqueue the plan `repeats` times; `ev` (optional) spans everything enqueued. */

@@ -74,14 +74,6 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
     return (uint32_t)__half_as_ushort(__float2half(lo)) | ((uint32_t)__half_as_ushort(__float2half(hi)) << 16);
 }
 
-// One tile of K and V in registers: lane chunk c = lane + 64 i (i < VI, c < D)
-// covers keys 4 (c % 8) .. +3 and dims 8 (c / 8) .. +7.
-template <int VI>
-struct TileRegs {
-    u32x4 k[VI][4];
-    u32x4 v[VI][4];
-};
-
 template <int KS, int DT, int NW>
 __global__ __launch_bounds__(64 * NW) void attention_kernel(const AttnArgs a) {
     using L = AttnLayout<KS, DT>;
@@ -106,52 +98,64 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(const AttnArgs a) {
         ks[key * L::KROW + d] = 0;
     }
 
+    // Raw buffer loads: an offset at or past num_records reads zeros, which
+    // covers keys past seq_kv, queries past seq_q and the idle lanes of a
+    // partial chunk round (offset 2^31) without branches around the loads.
+    const int row2 = (int)(row * 2);                      // bytes between consecutive positions
+    const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc((void*)a.Q, 0, a.seq_q * row2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc((void*)a.K, 0, a.seq_kv * row2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc((void*)a.V, 0, a.seq_kv * row2, 0x00020000);
+    constexpr uint32_t OOB = 0x80000000u;
+
     // Q fragments of this lane: Q[q][head][16 s + 8 h .. +7], zero past D / seq_q
     u32x4 qf[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
         const int d = 16 * s + 8 * h;
-        if (q < a.seq_q && d < D) qf[s] = *reinterpret_cast<const u32x4*>(a.Q + (int64_t)q * row + head * D + d);
-        else qf[s] = u32x4{0u, 0u, 0u, 0u};
+        const uint32_t off = q < a.seq_q && d < D ? (uint32_t)(q * row2 + (head * D + d) * 2) : OOB;
+        qf[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, (int)off, 0, 0));
     }
 
     const int shift = a.seq_kv - a.seq_q;
     const int last_key = a.causal ? min(a.seq_kv - 1, q + shift) : a.seq_kv - 1;   // lane's last visible key
+    // keys below this are visible to every query of the block
+    const int open_end = a.causal ? min(a.seq_kv, qb0 + shift + 1) : a.seq_kv;
     int kv_end = a.seq_kv;
     if (a.causal) kv_end = min(a.seq_kv, min(qb0 + 32, a.seq_q) + shift);
 
-    const uint16_t* kbase = a.K + head * D;
-    const uint16_t* vbase = a.V + head * D;
-    TileRegs<VI> tr;
+    // lane chunk c = lane + 64 i: keys 4 (c % 8) .. +3, dims 8 (c / 8) .. +7
+    uint32_t coff[VI];
+#pragma unroll
+    for (int i = 0; i < VI; ++i) {
+        const int c = lane + 64 * i;
+        coff[i] = c < D ? (uint32_t)(4 * (c & 7) * row2 + (head * D + 8 * (c >> 3)) * 2) : OOB;
+    }
+    u32x4 tk[VI][4], tv[VI][4];
     auto load_tile = [&](int kv0) {
+        const uint32_t base = (uint32_t)(kv0 * row2);
 #pragma unroll
-        for (int i = 0; i < VI; ++i) {
-            const int c = lane + 64 * i;
-            if (c < D) {
-                const int d = 8 * (c >> 3);
+        for (int i = 0; i < VI; ++i)
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int key = min(kv0 + 4 * (c & 7) + u, a.seq_kv - 1);
-                    tr.k[i][u] = *reinterpret_cast<const u32x4*>(kbase + (int64_t)key * row + d);
-                    tr.v[i][u] = *reinterpret_cast<const u32x4*>(vbase + (int64_t)key * row + d);
-                }
+            for (int u = 0; u < 4; ++u) {
+                const int off = (int)(coff[i] + base + u * row2);
+                tk[i][u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0));
+                tv[i][u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, off, 0, 0));
             }
-        }
     };
     auto store_tile = [&]() {
 #pragma unroll
         for (int i = 0; i < VI; ++i) {
             const int c = lane + 64 * i;
-            if (c < D) {
+            if (64 * i + 64 <= D || c < D) {
                 const int key0 = 4 * (c & 7), d = 8 * (c >> 3);
 #pragma unroll
-                for (int u = 0; u < 4; ++u) *reinterpret_cast<u32x4*>(ks + (key0 + u) * L::KROW + d) = tr.k[i][u];
+                for (int u = 0; u < 4; ++u) *reinterpret_cast<u32x4*>(ks + (key0 + u) * L::KROW + d) = tk[i][u];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     // dim d + j of keys key0 .. key0+3
                     const int sh = 16 * (j & 1);
-                    const uint32_t k01 = ((tr.v[i][0][j >> 1] >> sh) & 0xFFFFu) | (((tr.v[i][1][j >> 1] >> sh) & 0xFFFFu) << 16);
-                    const uint32_t k23 = ((tr.v[i][2][j >> 1] >> sh) & 0xFFFFu) | (((tr.v[i][3][j >> 1] >> sh) & 0xFFFFu) << 16);
+                    const uint32_t k01 = ((tv[i][0][j >> 1] >> sh) & 0xFFFFu) | (((tv[i][1][j >> 1] >> sh) & 0xFFFFu) << 16);
+                    const uint32_t k23 = ((tv[i][2][j >> 1] >> sh) & 0xFFFFu) | (((tv[i][3][j >> 1] >> sh) & 0xFFFFu) << 16);
                     *reinterpret_cast<u32x2*>(vt + (d + j) * L::VROW + key0) = u32x2{k01, k23};
                 }
             }
@@ -165,12 +169,14 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(const AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[t][r] = 0.0f;
 
+    // Tiles past kv_end are still loaded (as zeros or spare rows) so the loop
+    // body has no branch around its loads: the one in flight is never stored.
     int kv0 = 32 * wave;
-    if (kv0 < kv_end) load_tile(kv0);
+    load_tile(kv0);
     while (kv0 < kv_end) {
         store_tile();
         const int kv_next = kv0 + 32 * NW;
-        if (kv_next < kv_end) load_tile(kv_next);      // in flight while this tile computes
+        load_tile(kv_next);                               // in flight while this tile computes
         // this wave's own LDS: its stores above precede these reads in the wave's LDS order
         asm volatile("" ::: "memory");
 
@@ -182,18 +188,36 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(const AttnArgs a) {
             const u32x4 kf = *reinterpret_cast<const u32x4*>(ks + l32 * L::KROW + 16 * st + 8 * h);
             s = mfma_f16(kf, qf[st], s);
         }
-        float tmax = -INFINITY;
+        if (kv0 + 32 <= open_end) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int key = kv0 + 8 * (r >> 2) + 4 * h + (r & 3);
-            s[r] = key > last_key ? -INFINITY : s[r] * a.scale_log2;
-            tmax = fmaxf(tmax, s[r]);
+            for (int r = 0; r < 16; ++r) s[r] *= a.scale_log2;
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = kv0 + 8 * (r >> 2) + 4 * h + (r & 3);
+                s[r] = key > last_key ? -INFINITY : s[r] * a.scale_log2;
+            }
         }
+        float tmax = s[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, s[r]);
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float mnew = fmaxf(mrun, tmax);
-        // mnew stays -inf while every key so far is hidden from this query
-        const float msafe = mnew == -INFINITY ? 0.0f : mnew;
-        const float factor = __builtin_amdgcn_exp2f(mrun - msafe);
+        // Lazy rescaling: the reference point mrun moves only when a score
+        // exceeds it by more than 8 (probabilities stay <= 2^8, exact range
+        // for fp16), so most tiles skip the accumulator rescale.
+        if (__builtin_amdgcn_ballot_w64(tmax > mrun + 8.0f)) {
+            const float mnew = fmaxf(mrun, tmax);
+            // 0 when mrun = -inf; a lane that still sees no key keeps its zeros
+            const float factor = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(mrun - mnew);
+            lrun *= factor;
+#pragma unroll
+            for (int t = 0; t < DT; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) oacc[t][r] *= factor;
+            mrun = mnew;
+        }
+        // mrun stays -inf while every key so far is hidden from this query
+        const float msafe = mrun == -INFINITY ? 0.0f : mrun;
         float psum = 0.0f;
         float p[16];
 #pragma unroll
@@ -202,12 +226,7 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(const AttnArgs a) {
             psum += p[r];
         }
         psum += __shfl_xor(psum, 32, 64);
-        lrun = lrun * factor + psum;
-        mrun = mnew;
-#pragma unroll
-        for (int t = 0; t < DT; ++t)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) oacc[t][r] *= factor;
+        lrun += psum;
 
         // O^T += V^T P^T over the tile's two 16-key steps
 #pragma unroll

@@ -16,7 +16,7 @@ using namespace mvlm;
 
 namespace {
 
-enum OpKind { OP_GEMM_NAIVE, OP_GEMM_TILED, OP_GEMM_MFMA, OP_GEMV_DENSE, OP_GEMV_QUANT, OP_GEMV_GROUP, OP_ATTENTION };
+enum OpKind { OP_GEMM_NAIVE, OP_GEMM_TILED, OP_GEMM_MFMA, OP_GEMV_DENSE, OP_GEMV_QUANT, OP_GEMV_GROUP, OP_ATTENTION, OP_ARGMAX };
 
 struct Op {
     OpKind kind;
@@ -166,6 +166,10 @@ int make_attention(mvlm_device* dev, const mvlm_buffer* Q, const mvlm_buffer* K,
     REQUIRE(aligned16(Q->ptr) && aligned16(K->ptr) && aligned16(V->ptr) && aligned16(O->ptr),
             "%s: Q, K, V and O must be 16-byte aligned", fn);
     const size_t row = (size_t)heads * head_dim;
+    // the kernel addresses Q, K and V with 32-bit buffer offsets (keys read up
+    // to 576 positions past the end return zeros)
+    if ((size_t)seq_q * row * 2 > (1u << 30) || ((size_t)seq_kv + 576) * row * 2 > (1u << 30))
+        return set_error(MVLM_ERR_UNSUPPORTED, "%s: Q, K or V larger than 1 GiB", fn);
     NEED(Q, (size_t)seq_q * row * 2, "Q");
     NEED(K, (size_t)seq_kv * row * 2, "K");
     NEED(V, (size_t)seq_kv * row * 2, "V");
@@ -177,6 +181,24 @@ int make_attention(mvlm_device* dev, const mvlm_buffer* Q, const mvlm_buffer* K,
     op->causal = causal ? 1 : 0;
     op->scale = scale == 0.0f ? 1.0f / sqrtf((float)head_dim) : scale;
     op->num_cus = dev->prop.multiProcessorCount;
+    return MVLM_OK;
+}
+
+int make_argmax(mvlm_device* dev, const mvlm_buffer* x, int dtype, int rows, int n, int64_t ld,
+                mvlm_buffer* out, const char* fn, Op* op) {
+    REQUIRE(dev && x && out, "%s: null argument", fn);
+    REQUIRE(x->dev == dev && out->dev == dev, "%s: buffers belong to another device", fn);
+    REQUIRE(is_dense(dtype), "%s: dtype %d is not F32/F16/BF16", fn, dtype);
+    REQUIRE(rows > 0 && n > 0 && ld >= n, "%s: rows=%d n=%d ld=%lld", fn, rows, n, (long long)ld);
+    REQUIRE(rows <= (1 << 30), "%s: rows=%d too large", fn, rows);
+    NEED(x, ((size_t)(rows - 1) * ld + n) * dtype_size(dtype), "x");
+    NEED(out, (size_t)rows * 4, "out_index");
+    REQUIRE(((uintptr_t)out->ptr & 3u) == 0 && ((uintptr_t)x->ptr % dtype_size(dtype)) == 0,
+            "%s: misaligned buffer", fn);
+    op->kind = OP_ARGMAX;
+    op->a = x->ptr; op->c = out->ptr;
+    op->a_dtype = dtype;
+    op->M = rows; op->N = n; op->lda = ld;
     return MVLM_OK;
 }
 
@@ -258,6 +280,8 @@ hipError_t enqueue_op(hipStream_t s, const Op& op) {
                 return launch_gemv_stream(s, op.a, MVLM_F32, op.w, op.c, MVLM_F32, op.num_cus, &op.ep);
             return launch_gemm_skinny(s, (const float*)op.a, op.w, (float*)op.c, op.M, op.N, op.K, op.num_cus,
                                       &op.ep);
+        case OP_ARGMAX:
+            return launch_argmax(s, op.a, op.a_dtype, op.M, op.N, op.lda, (int*)op.c);
         case OP_ATTENTION:
             return launch_attention(s, op.a, op.b, op.v, op.c, op.c_dtype, op.M, op.N, op.batch, op.K, op.causal,
                                     op.scale, op.num_cus);
@@ -391,6 +415,12 @@ extern "C" int mvlm_attention_decode(mvlm_device* dev, const mvlm_buffer* Q, con
                        &op));
 }
 
+extern "C" int mvlm_argmax(mvlm_device* dev, const mvlm_buffer* x, int dtype, int rows, int n, int64_t ld,
+                           mvlm_buffer* out_index, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(make_argmax(dev, x, dtype, rows, n, ld, out_index, fn, &op));
+}
+
 // ---------------------------------------------------------------------------
 // plans
 // ---------------------------------------------------------------------------
@@ -504,6 +534,15 @@ extern "C" int mvlm_plan_add_attention(mvlm_plan* plan, const mvlm_buffer* Q, co
     Op op{};
     int st = make_attention(plan->dev, Q, K, V, O, o_dtype, seq_q, seq_kv, num_heads, head_dim, causal, scale, fn,
                             &op);
+    return st != MVLM_OK ? st : plan_push(plan, op);
+}
+
+extern "C" int mvlm_plan_add_argmax(mvlm_plan* plan, const mvlm_buffer* x, int dtype, int rows, int n, int64_t ld,
+                                    mvlm_buffer* out_index) {
+    const char* fn = __func__;
+    REQUIRE(plan, "%s: null argument", fn);
+    Op op{};
+    int st = make_argmax(plan->dev, x, dtype, rows, n, ld, out_index, fn, &op);
     return st != MVLM_OK ? st : plan_push(plan, op);
 }
 

@@ -116,6 +116,8 @@ _SIGNATURES = {
     "mvlm_attention_prefill": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, _PP]),
     "mvlm_attention_decode": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, _PP]),
     "mvlm_plan_add_attention": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int, c_int, c_float]),
+    "mvlm_argmax": (c_int, [_P, _P, c_int, c_int, c_int, c_int64, _P, _PP]),
+    "mvlm_plan_add_argmax": (c_int, [_P, _P, c_int, c_int, c_int, c_int64, _P]),
     "mvlm_fill_normal": (c_int, [_P, _P, c_int, c_size_t, c_uint64, c_double]),
     "mvlm_weight_random": (c_int, [_P, c_int, c_int, c_int, c_uint64, c_double, _PP]),
     "mvlm_event_wait": (c_int, [_P]),
@@ -432,6 +434,11 @@ class Plan:
         self._keep += [Q, K, V, O]
         return self
 
+    def add_argmax(self, x, dtype, rows, n, ld, out_index):
+        _call("mvlm_plan_add_argmax", self.handle, x.handle, dtype, rows, n, ld, out_index.handle)
+        self._keep += [x, out_index]
+        return self
+
     def use_graph(self, enable=True):
         _call("mvlm_plan_use_graph", self.handle, 1 if enable else 0)
         return self
@@ -585,6 +592,10 @@ class Device:
     def attention_decode(self, Q, K_cache, V_cache, O, cache_len, num_heads, head_dim, event=False):
         return self._launch("mvlm_attention_decode", (Q.handle, K_cache.handle, V_cache.handle, O.handle, cache_len,
                                                       num_heads, head_dim), event)
+
+    def argmax(self, x, dtype, rows, n, ld, out_index, event=False):
+        """out_index[r] (int32 on the device) = first index of the largest key of row r."""
+        return self._launch("mvlm_argmax", (x.handle, dtype, rows, n, ld, out_index.handle), event)
 
     def gemm_quant(self, X, W, Y, M, N, K, event=False):
         """Dispatch by the weight's dtype (Q8_0 or Q4_0)."""

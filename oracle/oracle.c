@@ -528,3 +528,66 @@ void orc_attention_f64(const uint16_t* Q, const uint16_t* K, const uint16_t* V, 
         free(q);
     }
 }
+
+int orc_argmax_f16_reference(const uint16_t* logits, int vocab) {
+    int best_id = 0;
+    float best_val = -1e30f;
+    for (int i = 0; i < vocab; i++) {
+        const uint16_t h = logits[i];
+        const uint32_t sign = (uint32_t)(h & 0x8000) << 16;
+        const uint32_t e = (h >> 10) & 0x1F, mant = h & 0x3FF;
+        float val;
+        if (e == 0) {
+            val = 0.0f;
+        } else if (e == 31) {
+            val = (sign ? -1.0f : 1.0f) * 1e30f;
+        } else {
+            const uint32_t f32 = sign | ((e - 15 + 127) << 23) | (mant << 13);
+            memcpy(&val, &f32, 4);
+        }
+        if (val > best_val) {
+            best_val = val;
+            best_id = i;
+        }
+    }
+    return best_id;
+}
+
+static float argmax_key(const void* row, long i, int dtype) {
+    if (dtype == 0) {
+        uint32_t b;
+        memcpy(&b, (const uint8_t*)row + 4 * i, 4);
+        const uint32_t e = (b >> 23) & 0xFF;
+        if (e == 0xFF) return (b >> 31) ? -INFINITY : INFINITY;
+        if (e == 0) return 0.0f;
+        float v;
+        memcpy(&v, &b, 4);
+        return v;
+    }
+    const uint16_t h = ((const uint16_t*)row)[i];
+    if (dtype == 1) {
+        const uint32_t e = (h >> 10) & 0x1F;
+        if (e == 0x1F) return (h >> 15) ? -INFINITY : INFINITY;
+        return e == 0 ? 0.0f : orc_f16_to_f32(h);
+    }
+    const uint32_t e = (h >> 7) & 0xFF;
+    if (e == 0xFF) return (h >> 15) ? -INFINITY : INFINITY;
+    return e == 0 ? 0.0f : orc_bf16_to_f32(h);
+}
+
+void orc_argmax(const void* x, int dtype, int rows, int n, long ld, int* out) {
+    const size_t es = dtype == 0 ? 4 : 2;
+    for (int r = 0; r < rows; ++r) {
+        const void* row = (const uint8_t*)x + (size_t)r * ld * es;
+        int best = 0;
+        float bk = argmax_key(row, 0, dtype);
+        for (int i = 1; i < n; ++i) {
+            const float k = argmax_key(row, i, dtype);
+            if (k > bk) {
+                bk = k;
+                best = i;
+            }
+        }
+        out[r] = best;
+    }
+}

@@ -24,6 +24,7 @@
  *                    tolerance |y - r| <= rtol * scale.
  *   orc_attention_f64  src/kernels/attention.cl:46-179 / :197-295 (softmax(Q K^T
  *                    / sqrt(d) + causal mask) V per head) in fp64.
+ *   orc_argmax*      src/models/moondream2.cpp:553-593 (host argmax of the logits).
  *
  * Pinning (each function has at least one check that does not retype it):
  * golden fixtures under tests/golden/, closed forms (one-hot, identity,
@@ -119,6 +120,14 @@ void orc_epilogue_f64(double* Y, const double* bias, const double* mul, const do
  * R[q][h] = max_k scale * sum_d |Q[d] K[k][d]| (the error scale of a score). */
 void orc_attention_f64(const uint16_t* Q, const uint16_t* K, const uint16_t* V, double* O, double* A, double* R,
                        int seq_q, int seq_kv, int heads, int D, int causal, double scale, int nthreads);
+
+/* ---- LM-head token pick (src/models/moondream2.cpp:553-593) ---------------
+ * orc_argmax_f16_reference: the reference's scan, literally: fp16 decode with
+ * zero exponent -> 0 and all-ones exponent -> +-1e30, best = -1e30, strict '>'
+ * from index 0.  orc_argmax: the same order for F32 (0), F16 (1) and BF16 (30)
+ * rows with inf/NaN as +-inf; out[r] for each of `rows` rows of stride ld. */
+int orc_argmax_f16_reference(const uint16_t* logits, int vocab);
+void orc_argmax(const void* x, int dtype, int rows, int n, long ld, int* out);
 
 int orc_max_threads(void);
 

@@ -69,6 +69,8 @@ def lib():
                                             ctypes.c_long, ctypes.c_long, ctypes.c_long]),
             "orc_gemm_f64_nk": (None, [_f64p, _f64p, _f64p, _f64p, i, i, i, i]),
             "orc_max_threads": (i, []),
+            "orc_argmax_f16_reference": (i, [_u16p, i]),
+            "orc_argmax": (None, [ctypes.c_void_p, i, i, i, ctypes.c_long, np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")]),
             "orc_attention_f64": (None, [_u16p, _u16p, _u16p, _f64p, _f64p, _f64p, i, i, i, i, i, d, i]),
             "orc_gelu_tanh": (d, [d]),
             "orc_silu": (d, [d]),
@@ -247,3 +249,11 @@ def attention_f64(Q, K, V, seq_q, seq_kv, heads, D, causal=False, scale=None, nt
                             np.ascontiguousarray(V, np.uint16).ravel(), O, A, R, seq_q, seq_kv, heads, D,
                             1 if causal else 0, float(scale), nthreads)
     return O.reshape(seq_q, heads, D), A.reshape(seq_q, heads, D), R.reshape(seq_q, heads)
+
+
+def argmax(x, dtype, rows, n, ld):
+    """row-wise first index of the largest key (x: float32 array or uint16 bits)."""
+    x = np.ascontiguousarray(x)
+    out = np.empty(rows, np.int32)
+    lib().orc_argmax(x.ctypes.data, dtype, rows, n, ld, out)
+    return out

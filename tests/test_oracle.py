@@ -375,3 +375,65 @@ def test_attention_heads_are_independent(orc):
     O, _, _ = orc.attention_f64(Q, K, V, S, S, H, D, causal=True)
     Op, _, _ = orc.attention_f64(Q[:, perm], K[:, perm], V[:, perm], S, S, H, D, causal=True)
     assert np.array_equal(Op, O[:, perm])
+
+
+# ---- LM-head token pick (moondream2.cpp:553-593) ------------------------------
+
+F32_ID, F16_ID, BF16_ID = 0, 1, 30
+
+
+def _bf16_bits(v32):
+    return (np.asarray(v32, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def test_argmax_distinct_values_match_numpy(orc):
+    rng = np.random.default_rng(21)
+    rows, n = 5, 3001
+    x = rng.permutation(rows * n).astype(np.float32).reshape(rows, n) - 7000.0    # distinct, exact in fp32
+    assert np.array_equal(orc.argmax(x, F32_ID, rows, n, n), np.argmax(x, axis=1))
+    h = rng.permutation(2000).astype(np.float16)[:1999] - np.float16(1000)       # distinct, exact in fp16
+    assert orc.argmax(h.view(np.uint16), F16_ID, 1, h.size, h.size)[0] == int(np.argmax(h))
+    b = _bf16_bits(x)                                                           # ties possible: first wins
+    vals = (b.astype(np.uint32) << 16).view(np.float32)
+    want = [int(np.flatnonzero(r == r.max())[0]) for r in vals]
+    assert orc.argmax(b, BF16_ID, rows, n, n).tolist() == want
+
+
+def test_argmax_keys_and_ties(orc):
+    def f16(vals):
+        return np.array(vals, np.float16).view(np.uint16)
+    neg_sub = np.uint16(0x8001)                              # -smallest subnormal: counts as +0
+    cases = [
+        (f16([1.0, 3.0, 3.0, 2.0]), 1),                      # first of equal maxima
+        (f16([-np.inf, -np.inf]), 0),                        # nothing beats the start
+        (f16([-1.0, np.inf, 5.0, np.inf]), 1),
+        (f16([0.5, np.nan]), 1),                             # +NaN is +inf
+        (np.array([0x3C00, 0xFE00], np.uint16), 0),          # -NaN is -inf
+        (np.array([neg_sub, 0x0000], np.uint16), 0),         # subnormal == 0: first wins
+        (np.array([0x8000, 0x0001, 0x0000], np.uint16), 0),  # -0, +subnormal, +0 all equal
+        (f16([-2.0, -np.inf, -1.5]), 2),
+    ]
+    for bits, want in cases:
+        assert orc.lib().orc_argmax_f16_reference(bits, bits.size) == want, bits
+        assert orc.argmax(bits, F16_ID, 1, bits.size, bits.size)[0] == want, bits
+    f = np.array([1e38, np.inf, 3.0], np.float32)
+    assert orc.argmax(f, F32_ID, 1, 3, 3)[0] == 1
+    f = np.array([np.float32(1e-40), 0.0, -1e-40], np.float32)   # fp32 subnormals count as 0
+    assert orc.argmax(f, F32_ID, 1, 3, 3)[0] == 0
+
+
+def test_argmax_generalised_key_equals_reference_scan_on_f16(orc):
+    rng = np.random.default_rng(22)
+    for trial in range(20):
+        bits = rng.integers(0, 1 << 16, 4096, dtype=np.uint16)     # every class: NaN, inf, subnormal, ±0
+        if trial % 2:
+            bits[rng.integers(0, 4096, 50)] = 0x7C00
+        assert orc.argmax(bits, F16_ID, 1, bits.size, bits.size)[0] == \
+            orc.lib().orc_argmax_f16_reference(bits, bits.size)
+
+
+def test_argmax_rows_and_stride(orc):
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal((4, 100)).astype(np.float32)
+    got = orc.argmax(x, F32_ID, 3, 60, 100)                    # 3 rows of 60, stride 100
+    assert got.tolist() == np.argmax(x[:3, :60], axis=1).tolist()
