@@ -17,22 +17,19 @@
 namespace mvlm {
 
 template <int DT>
-__device__ __forceinline__ float argmax_key(const void* row, int64_t i) {
+__device__ __forceinline__ float argmax_key_bits(uint32_t b) {
     if constexpr (DT == MVLM_F32) {
-        const uint32_t b = ((const uint32_t*)row)[i];
         const uint32_t e = (b >> 23) & 0xFFu;
         if (e == 0xFFu) return (b >> 31) ? -INFINITY : INFINITY;
         return e == 0 ? 0.0f : __uint_as_float(b);
     } else if constexpr (DT == MVLM_F16) {
-        const uint16_t h = ((const uint16_t*)row)[i];
-        const uint32_t e = (h >> 10) & 0x1Fu;
-        if (e == 0x1Fu) return (h >> 15) ? -INFINITY : INFINITY;
-        return e == 0 ? 0.0f : f16_bits_to_f32(h);
+        const uint32_t e = (b >> 10) & 0x1Fu;
+        if (e == 0x1Fu) return ((b >> 15) & 1u) ? -INFINITY : INFINITY;
+        return e == 0 ? 0.0f : f16_bits_to_f32((uint16_t)b);
     } else {
-        const uint16_t h = ((const uint16_t*)row)[i];
-        const uint32_t e = (h >> 7) & 0xFFu;
-        if (e == 0xFFu) return (h >> 15) ? -INFINITY : INFINITY;
-        return e == 0 ? 0.0f : bf16_bits_to_f32(h);
+        const uint32_t e = (b >> 7) & 0xFFu;
+        if (e == 0xFFu) return ((b >> 15) & 1u) ? -INFINITY : INFINITY;
+        return e == 0 ? 0.0f : bf16_bits_to_f32((uint16_t)b);
     }
 }
 
@@ -41,19 +38,58 @@ __device__ __forceinline__ bool argmax_better(float k, int i, float bk, int bi) 
 }
 
 constexpr int ARGMAX_THREADS = 1024;
+constexpr int ARGMAX_BATCH = 8;       // 16-byte chunks in flight per thread
 
+// element e of a 16-byte chunk
 template <int DT>
+__device__ __forceinline__ uint32_t chunk_elem(const u32x4& c, int e) {
+    if constexpr (DT == MVLM_F32) return c[e];
+    else return (c[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+}
+
+// One workgroup per row.  VEC: the row starts 16-byte aligned and is read in
+// 16-byte chunks (ARGMAX_BATCH per thread in flight); the last n % EPC
+// elements, and every element when !VEC, are read one at a time.  Each thread
+// visits its indices in increasing order, so its candidate is the first of
+// its largest keys; the reductions break ties by the smaller index.
+template <int DT, bool VEC>
 __global__ __launch_bounds__(ARGMAX_THREADS) void argmax_kernel(const void* x, int n, int64_t ld, int* out) {
     __shared__ float wk[ARGMAX_THREADS / 64];
     __shared__ int wi[ARGMAX_THREADS / 64];
-    const int es = DT == MVLM_F32 ? 4 : 2;
-    const void* row = (const uint8_t*)x + (int64_t)blockIdx.x * ld * es;
-    // each thread visits its indices in increasing order: strict '>' keeps the first
+    constexpr int ES = DT == MVLM_F32 ? 4 : 2;
+    constexpr int EPC = 16 / ES;
+    const uint8_t* row = (const uint8_t*)x + (int64_t)blockIdx.x * ld * ES;
     float bk = -INFINITY;
     int bi = 0x7FFFFFFF;
-    for (int i = threadIdx.x; i < n; i += ARGMAX_THREADS) {
-        const float k = argmax_key<DT>(row, i);
-        if (bi == 0x7FFFFFFF || k > bk) {
+    int scalar_from = 0;
+    if constexpr (VEC) {
+        const int nchunks = n / EPC;
+        const u32x4* chunks = (const u32x4*)row;
+        for (int base = threadIdx.x; base < nchunks; base += ARGMAX_THREADS * ARGMAX_BATCH) {
+            u32x4 c[ARGMAX_BATCH];
+#pragma unroll
+            for (int u = 0; u < ARGMAX_BATCH; ++u) c[u] = chunks[min(base + u * ARGMAX_THREADS, nchunks - 1)];
+#pragma unroll
+            for (int u = 0; u < ARGMAX_BATCH; ++u) {
+                const int ci = base + u * ARGMAX_THREADS;
+                if (ci < nchunks) {
+#pragma unroll
+                    for (int e = 0; e < EPC; ++e) {
+                        const float k = argmax_key_bits<DT>(chunk_elem<DT>(c[u], e));
+                        if (argmax_better(k, ci * EPC + e, bk, bi)) {
+                            bk = k;
+                            bi = ci * EPC + e;
+                        }
+                    }
+                }
+            }
+        }
+        scalar_from = nchunks * EPC;
+    }
+    for (int i = scalar_from + threadIdx.x; i < n; i += ARGMAX_THREADS) {
+        const uint32_t b = ES == 4 ? ((const uint32_t*)row)[i] : ((const uint16_t*)row)[i];
+        const float k = argmax_key_bits<DT>(b);
+        if (argmax_better(k, i, bk, bi)) {
             bk = k;
             bi = i;
         }
@@ -83,12 +119,20 @@ __global__ __launch_bounds__(ARGMAX_THREADS) void argmax_kernel(const void* x, i
     }
 }
 
-hipError_t launch_argmax(hipStream_t s, const void* x, int dtype, int rows, int n, int64_t ld, int* out) {
+template <int DT>
+static void launch_dt(hipStream_t s, const void* x, int rows, int n, int64_t ld, int* out) {
+    constexpr int ES = DT == MVLM_F32 ? 4 : 2;
+    const bool vec = ((uintptr_t)x & 15u) == 0 && (ld * ES) % 16 == 0;
     const dim3 grid((unsigned)rows), block(ARGMAX_THREADS);
+    if (vec) launch_kernel(argmax_kernel<DT, true>, grid, block, 0, s, x, n, ld, out);
+    else launch_kernel(argmax_kernel<DT, false>, grid, block, 0, s, x, n, ld, out);
+}
+
+hipError_t launch_argmax(hipStream_t s, const void* x, int dtype, int rows, int n, int64_t ld, int* out) {
     switch (dtype) {
-        case MVLM_F32: launch_kernel(argmax_kernel<MVLM_F32>, grid, block, 0, s, x, n, ld, out); break;
-        case MVLM_F16: launch_kernel(argmax_kernel<MVLM_F16>, grid, block, 0, s, x, n, ld, out); break;
-        case MVLM_BF16: launch_kernel(argmax_kernel<MVLM_BF16>, grid, block, 0, s, x, n, ld, out); break;
+        case MVLM_F32: launch_dt<MVLM_F32>(s, x, rows, n, ld, out); break;
+        case MVLM_F16: launch_dt<MVLM_F16>(s, x, rows, n, ld, out); break;
+        case MVLM_BF16: launch_dt<MVLM_BF16>(s, x, rows, n, ld, out); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

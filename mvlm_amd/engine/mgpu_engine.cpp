@@ -152,6 +152,33 @@ Event dispatch_gemv_quant(const DeviceInfo* dev, Program, Buffer x, Weight W, Bu
     return ok(st, "dispatch_gemv_quant") ? ev : nullptr;
 }
 
+Event dispatch_attention_prefill(const DeviceInfo* dev, Program, Buffer Q, Buffer K, Buffer V, Buffer output,
+                                 int seq_len, int num_heads, int head_dim) {
+    if (!dev) return nullptr;
+    mvlm_event* ev = nullptr;
+    int st = mvlm_attention_prefill(dev->device, Q, K, V, output, seq_len, num_heads, head_dim, &ev);
+    return ok(st, "dispatch_attention_prefill") ? ev : nullptr;
+}
+
+Event dispatch_attention_decode(const DeviceInfo* dev, Program, Buffer Q, Buffer K_cache, Buffer V_cache,
+                                Buffer output, int cache_len, int num_heads, int head_dim) {
+    if (!dev) return nullptr;
+    mvlm_event* ev = nullptr;
+    int st = mvlm_attention_decode(dev->device, Q, K_cache, V_cache, output, cache_len, num_heads, head_dim, &ev);
+    return ok(st, "dispatch_attention_decode") ? ev : nullptr;
+}
+
+int argmax_logits(const DeviceInfo* dev, Buffer logits, int vocab_size) {
+    if (!dev) return -1;
+    mvlm_buffer* out = nullptr;
+    if (!ok(mvlm_buffer_alloc(dev->device, 4, &out), "argmax_logits")) return -1;
+    int32_t id = -1;
+    bool good = ok(mvlm_argmax(dev->device, logits, MVLM_F16, 1, vocab_size, vocab_size, out, nullptr), "argmax_logits") &&
+                ok(mvlm_buffer_download(out, 0, &id, 4), "argmax_logits");
+    mvlm_buffer_free(out);
+    return good ? id : -1;
+}
+
 bool wait_event(Event ev) { return ev && ok(mvlm_event_wait(ev), "wait_event"); }
 
 double event_elapsed_ms(Event ev) {

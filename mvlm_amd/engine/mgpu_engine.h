@@ -76,6 +76,14 @@ Event dispatch_gemm_image(const DeviceInfo* dev, Program program, Buffer A, Weig
 Event dispatch_gemv(const DeviceInfo* dev, Program program, Buffer x, Weight W_img, Buffer y, int N, int K);
 // The dequantizing GEMV of README.md:57 (fp32 x and y, Q8_0 / Q4_0 weights), M <= 16 rows.
 Event dispatch_gemv_quant(const DeviceInfo* dev, Program program, Buffer x, Weight W, Buffer y, int M, int N, int K);
+// src/engine/compute.h:65-73 (fused MFMA attention; fp16 [seq][heads][head_dim])
+Event dispatch_attention_prefill(const DeviceInfo* dev, Program program, Buffer Q, Buffer K, Buffer V, Buffer output,
+                                 int seq_len, int num_heads, int head_dim);
+Event dispatch_attention_decode(const DeviceInfo* dev, Program program, Buffer Q, Buffer K_cache, Buffer V_cache,
+                                Buffer output, int cache_len, int num_heads, int head_dim);
+// replaces argmax_logits (src/models/moondream2.cpp:553-593): the token id of
+// the largest fp16 logit, picked on the device (4 bytes read back); -1 on error
+int argmax_logits(const DeviceInfo* dev, Buffer logits, int vocab_size);
 
 // cl_event handling: clWaitForEvents + profiling read + clReleaseEvent.
 bool wait_event(Event ev);

@@ -127,6 +127,49 @@ static void test_quant_gemv(const DeviceInfo* dev) {
     release_buffer(dx); release_buffer(dy);
 }
 
+static void test_attention_and_token_pick(const DeviceInfo* dev) {
+    std::printf("dispatch_attention_prefill / _decode and argmax_logits\n");
+    // Q = 0 makes every visible score equal: the output is the mean of the
+    // visible V rows (prefix means for the causal prefill, the full mean for
+    // decode); small-integer V, fp16 output within half an ulp of the mean
+    const int S = 8, H = 2, D = 64;
+    std::vector<uint16_t> Q(S * H * D, 0), V(S * H * D), O(S * H * D);
+    for (int i = 0; i < S * H * D; ++i) V[i] = h((float)((i * 7) % 11 - 5));
+    Buffer dQ = create_buffer(dev, Q.size() * 2, 0, Q.data());
+    Buffer dK = create_buffer(dev, V.size() * 2, 0, V.data());     // any finite keys
+    Buffer dV = create_buffer(dev, V.size() * 2, 0, V.data());
+    Buffer dO = create_buffer(dev, O.size() * 2);
+    Event ev = dispatch_attention_prefill(dev, nullptr, dQ, dK, dV, dO, S, H, D);
+    EXPECT_TRUE(ev && wait_event(ev));
+    release_event(ev);
+    EXPECT_TRUE(read_buffer(dev, dO, 0, O.size() * 2, O.data()));
+    int bad = 0;
+    for (int q = 0; q < S; ++q)
+        for (int j = 0; j < H * D; ++j) {
+            float sum = 0.0f;
+            for (int k = 0; k <= q; ++k) sum += f(V[k * H * D + j]);
+            const float want = sum / (float)(q + 1);
+            bad += std::fabs(f(O[q * H * D + j]) - want) > std::fabs(want) * 1e-3f + 1e-6f;
+        }
+    EXPECT_EQ(bad, 0);
+    ev = dispatch_attention_decode(dev, nullptr, dQ, dK, dV, dO, S, H, D);   // query = row 0 of Q
+    EXPECT_TRUE(ev && wait_event(ev));
+    release_event(ev);
+    EXPECT_TRUE(read_buffer(dev, dO, 0, H * D * 2, O.data()));
+    for (int j = 0; j < H * D; ++j) {
+        float sum = 0.0f;
+        for (int k = 0; k < S; ++k) sum += f(V[k * H * D + j]);
+        EXPECT_TRUE(std::fabs(f(O[j]) - sum / S) <= std::fabs(sum / S) * 1e-3f + 1e-6f);
+    }
+    // token pick: the first of two equal maxima
+    std::vector<uint16_t> logits(51200);
+    for (int i = 0; i < 51200; ++i) logits[i] = h((float)(i % 97 - 60));
+    logits[31000] = logits[40000] = h(100.0f);
+    Buffer dl = create_buffer(dev, logits.size() * 2, 0, logits.data());
+    EXPECT_EQ(argmax_logits(dev, dl, 51200), 31000);
+    release_buffer(dQ); release_buffer(dK); release_buffer(dV); release_buffer(dO); release_buffer(dl);
+}
+
 int main() {
     DeviceInfo dev;
     if (!init_device(&dev)) {
@@ -137,6 +180,7 @@ int main() {
     test_buffer_pool(&dev);
     test_gemm_variants(&dev);
     test_quant_gemv(&dev);
+    test_attention_and_token_pick(&dev);
     EXPECT_TRUE(finish(&dev));
     destroy_device(&dev);
     std::printf(g_failures ? "FAILED (%d)\n" : "PASSED\n", g_failures);

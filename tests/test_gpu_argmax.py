@@ -56,6 +56,18 @@ def test_argmax_ties_and_specials(dev, orc, dt):
     assert got.tolist() == [70, 0, 123, 777, 0, 0]
 
 
+@pytest.mark.parametrize("dt", [m.F32, m.F16, m.BF16])
+def test_argmax_aligned_rows_with_tail(dev, orc, dt):
+    """16-byte rows read in chunks, then n % (16 / size) trailing elements one at a time"""
+    rows, n, ld = 3, 51197, 51200
+    rng = np.random.default_rng(8)
+    v = rng.standard_normal(rows * ld).astype(np.float32)
+    v[n - 1] = 50.0                                      # row 0: the winner is a tail element
+    v[ld + 7] = v[ld + n - 2] = 60.0                     # row 1: tie between a chunk and a tail element
+    got = run(dev, orc, bits_for(v, dt), dt, rows, n, ld)
+    assert got[0] == n - 1 and got[1] == 7
+
+
 def test_argmax_f16_subnormals_and_stride(dev, orc):
     n, ld, rows = 4000, 4096, 3
     rng = np.random.default_rng(6)
