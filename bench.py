@@ -8,9 +8,10 @@ decode step over Q8_0 weights -- 24 layers x {QKV 2048->6144, dense
 A step is one pass of the 97 GEMVs, enqueued from native code as a replayed
 HIP graph.  The other configurations (Q4_0 at M = 1, 4, 16; the fp32 GEMV;
 the M = 768 Phi-1.5 prefill GEMMs; the 729-token SigLIP GEMMs and the batched
-Q*K^T) are reported under "extra" with their own roofline fractions.
+Q*K^T; fused attention and the LM-head token pick) are reported under "extra"
+with their own roofline fractions.
 
-    python bench.py [--steps K] [--warmup W] [--quick] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--quick] [--no-cpu] [--attention-only]
 """
 from __future__ import annotations
 
@@ -191,6 +192,67 @@ def qk_batched(dev, m, steps, warmup):
     return res
 
 
+ATTENTION_SHAPES = [
+    # name, seq_q, seq_kv, heads, head_dim, causal
+    ("siglip_attention_16x729x72", 729, 729, 16, 72, False),
+    ("phi15_prefill_attention_768_causal", 768, 768, 32, 64, True),
+    ("phi15_decode_attention_cache2048", 1, 2048, 32, 64, False),
+]
+
+
+def attention_shape(dev, m, name, sq, skv, H, D, causal, steps, warmup):
+    """Fused attention, fp16 Q/K/V ~ N(0,1) in [seq][heads][head_dim], fp16 out.
+    flops = 4 H sq skv D (QK^T and PV; half of it under a square causal mask);
+    bytes = Q + K + V + O once each."""
+    n = sq * H * D
+    Q = dev.fill_normal(dev.alloc(n * 2), m.F16, n, SEED ^ 0x501, 1.0)
+    K = dev.fill_normal(dev.alloc(skv * H * D * 2), m.F16, skv * H * D, SEED ^ 0x502, 1.0)
+    V = dev.fill_normal(dev.alloc(skv * H * D * 2), m.F16, skv * H * D, SEED ^ 0x503, 1.0)
+    O = dev.alloc(n * 2)
+    plan = m.Plan(dev)
+    plan.add_attention(Q, K, V, O, m.F16, sq, skv, H, D, causal=causal)
+    per_op = profile_plan(plan)
+    plan.use_graph(True)
+    ms = timed_plan(dev, plan, steps, warmup)
+    frac_causal = (1.0 - (sq - 1) / (2.0 * skv)) if causal else 1.0
+    flops = 4.0 * H * sq * skv * D * frac_causal
+    nbytes = 2.0 * (2 * sq * H * D + 2 * skv * H * D)
+    kus = float(per_op[0]) * 1e3
+    res = {"workload": name, "shape": [sq, skv, H, D, int(causal)], "us": ms * 1e3, "kernel_us": kus,
+           "tflops": flops / kus / 1e6, "gbs": nbytes / kus / 1e3}
+    res["frac_mfma"] = res["tflops"] / PEAK_F16_TFLOPS
+    res["frac_hbm"] = res["gbs"] / PEAK_HBM_GBS
+    plan.destroy()
+    return res
+
+
+def token_pick(dev, m, steps, warmup):
+    """Row argmax of 51200 fp32 logits (the LM-head token pick)."""
+    n = PHI_LM_HEAD[1]
+    x = dev.fill_normal(dev.alloc(n * 4), m.F32, n, SEED ^ 0x601, 1.0)
+    out = dev.alloc(4)
+    plan = m.Plan(dev)
+    plan.add_argmax(x, m.F32, 1, n, n, out)
+    per_op = profile_plan(plan)
+    plan.use_graph(True)
+    ms = timed_plan(dev, plan, steps, warmup)
+    kus = float(per_op[0]) * 1e3
+    res = {"workload": "token_pick_51200_f32", "us": ms * 1e3, "kernel_us": kus, "gbs": 4.0 * n / kus / 1e3}
+    plan.destroy()
+    return res
+
+
+def f4_extras(dev, m, steps, warmup, extra):
+    for name, sq, skv, H, D, causal in ATTENTION_SHAPES:
+        r = attention_shape(dev, m, name, sq, skv, H, D, causal, steps, warmup)
+        extra[name] = r
+        log(f"[bench]   {name}: {r['kernel_us']:.1f} us kernel ({r['us']:.1f} us in graph) "
+            f"{r['tflops']:.0f} TFLOP/s ({100 * r['frac_mfma']:.1f}% of 2.5 PF) {r['gbs']:.0f} GB/s")
+    r = token_pick(dev, m, steps, warmup)
+    extra[r["workload"]] = r
+    log(f"[bench]   {r['workload']}: {r['kernel_us']:.1f} us kernel ({r['us']:.1f} us in graph)")
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline: the oracle's Q8_0 GEMV on the host cores
 # ---------------------------------------------------------------------------
@@ -310,6 +372,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="enqueue plans eagerly instead of replaying HIP graphs")
     ap.add_argument("--pmc-probe", action="store_true", help="workload for rocprofv3 --pmc traffic runs")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="only the attention and token-pick workloads (one JSON line of them)")
     ap.add_argument("--pmc-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn the two counter runs into " + os.path.relpath(TRAFFIC_FILE, ROOT))
     args = ap.parse_args()
@@ -329,6 +393,12 @@ def main():
     info = dev.info()
     log(f"[bench] {info.device_name.decode()} {info.arch_name.decode()} CUs={info.compute_units} "
         f"clock={info.max_clock_mhz} MHz HBM={info.global_mem_size / 2**30:.0f} GiB")
+    if args.attention_only:
+        extra = {}
+        f4_extras(dev, m, 20, 5, extra)
+        dev.close()
+        print(json.dumps({"workloads": extra}), flush=True)
+        return
 
     log("[bench] headline: phi15 decode step, Q8_0, M=1")
     head = decode_step(dev, m, "q8_0", 1, args.steps, args.warmup, graph=not args.eager)
@@ -357,6 +427,7 @@ def main():
         r = qk_batched(dev, m, 20, 5)
         extra[r["workload"]] = r
         log(f"[bench]   {r['workload']}: {r['us']:.1f} us {r['tflops']:.0f} TFLOP/s {r['gbs']:.0f} GB/s")
+        f4_extras(dev, m, 20, 5, extra)
 
     cpu = None
     if not args.no_cpu:

@@ -38,6 +38,7 @@
 #include "device_math.h"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace mvlm {
 
@@ -50,7 +51,23 @@ struct AttnArgs {
     int seq_q, seq_kv, heads, D;
     int causal;
     float scale_log2;      // scale * log2(e): scores are kept in the exp2 domain
+    // split over keys (blockIdx.z = split): each split covers tiles_per_split
+    // key tiles and, when splits > 1, parks (m, l) and the unnormalized output
+    // in ws for attention_combine_kernel
+    int splits, tiles_per_split;
+    float* ws;
 };
+
+// Partial results of split s for (query q, head h), record r = (s seq_q + q) heads + h:
+// ws[r D ..] = D floats of unnormalized output; after all splits seq_q heads
+// records, ws[.. + 2 r], [.. + 2 r + 1] = running max (exp2 domain) and sum.
+__device__ __forceinline__ int64_t attn_record(const AttnArgs& a, int split, int q, int head) {
+    return ((int64_t)split * a.seq_q + q) * a.heads + head;
+}
+__device__ __forceinline__ float* attn_ws_out(const AttnArgs& a, int64_t r) { return a.ws + r * a.D; }
+__device__ __forceinline__ float* attn_ws_ml(const AttnArgs& a, int64_t r) {
+    return a.ws + (int64_t)a.splits * a.seq_q * a.heads * a.D + 2 * r;
+}
 
 template <int KS, int DT>
 struct AttnLayout {
@@ -169,11 +186,14 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(const AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[t][r] = 0.0f;
 
-    // Tiles past kv_end are still loaded (as zeros or spare rows) so the loop
+    // This block's keys: tiles [split * tiles_per_split, +tiles_per_split) below kv_end.
+    // Tiles past the end are still loaded (as zeros or spare rows) so the loop
     // body has no branch around its loads: the one in flight is never stored.
-    int kv0 = 32 * wave;
+    const int split = blockIdx.z;
+    const int kv_stop = min(kv_end, 32 * (split + 1) * a.tiles_per_split);
+    int kv0 = 32 * (split * a.tiles_per_split + wave);
     load_tile(kv0);
-    while (kv0 < kv_end) {
+    while (kv0 < kv_stop) {
         store_tile();
         const int kv_next = kv0 + 32 * NW;
         load_tile(kv_next);                               // in flight while this tile computes
@@ -256,6 +276,21 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(const AttnArgs a) {
 
     if constexpr (NW == 1) {
         if (q >= a.seq_q) return;
+        if (a.splits > 1) {
+            const int64_t r = attn_record(a, split, q, head);
+            float* wo = attn_ws_out(a, r);
+#pragma unroll
+            for (int t = 0; t < DT; ++t)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int d = 32 * t + 8 * g + 4 * h;
+                    if (d < D)
+                        *reinterpret_cast<f32x4*>(wo + d) =
+                            f32x4{oacc[t][4 * g], oacc[t][4 * g + 1], oacc[t][4 * g + 2], oacc[t][4 * g + 3]};
+                }
+            if (h == 0) *reinterpret_cast<f32x2*>(attn_ws_ml(a, r)) = f32x2{mrun, lrun};
+            return;
+        }
         const float inv = 1.0f / lrun;
 #pragma unroll
         for (int t = 0; t < DT; ++t)
@@ -293,19 +328,70 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(const AttnArgs a) {
                 mw[w] = ((const float*)(lds + w * L::REGION))[32 * L::OPITCH + ql];
                 mx = fmaxf(mx, mw[w]);
             }
+            // a split's keys may all be hidden from a query (causal): m = -inf in
+            // every wave; the record then keeps m = -inf with l = 0, O = 0
+            const float mref = mx == -INFINITY ? 0.0f : mx;
             float lsum = 0.0f;
             f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int w = 0; w < NW; ++w) {
                 const float* rw = (const float*)(lds + w * L::REGION);
-                const float f = __builtin_amdgcn_exp2f(mw[w] - mx);
+                const float f = __builtin_amdgcn_exp2f(mw[w] - mref);
                 lsum += f * rw[32 * L::OPITCH + 32 + ql];
                 o += f * *reinterpret_cast<const f32x4*>(rw + ql * L::OPITCH + d);
+            }
+            if (a.splits > 1) {
+                const int64_t r = attn_record(a, split, qb0 + ql, head);
+                *reinterpret_cast<f32x4*>(attn_ws_out(a, r) + d) = o;
+                if (d == 0) *reinterpret_cast<f32x2*>(attn_ws_ml(a, r)) = f32x2{mx, lsum};
+                continue;
             }
             const float inv = 1.0f / lsum;
             store4(qb0 + ql, d, o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv);
         }
     }
+}
+
+// Merges the splits' partial softmaxes: thread = (query, head, 4 dims).  The
+// records are read 8 at a time (all loads in flight together) and folded in
+// with an online rescale, so no pass over the maxima comes first.
+__global__ __launch_bounds__(256) void attention_combine_kernel(const AttnArgs a) {
+    constexpr int BATCH = 8;
+    const int64_t item = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int d4 = a.D / 4;
+    if (item >= (int64_t)a.seq_q * a.heads * d4) return;
+    const int64_t qh = item / d4;                          // q * heads + head
+    const int d = 4 * (int)(item - qh * d4);
+    const int64_t stride = (int64_t)a.seq_q * a.heads;     // records between splits
+    float mx = -INFINITY, lsum = 0.0f;
+    f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < a.splits; s0 += BATCH) {
+        f32x2 ml[BATCH];
+        f32x4 ov[BATCH];
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+            const int64_t r = min(s0 + u, a.splits - 1) * stride + qh;
+            ml[u] = *reinterpret_cast<const f32x2*>(attn_ws_ml(a, r));
+            ov[u] = *reinterpret_cast<const f32x4*>(attn_ws_out(a, r) + d);
+        }
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+            if (s0 + u >= a.splits || ml[u][0] == -INFINITY) continue;   // past the end, or saw no key
+            const float mn = fmaxf(mx, ml[u][0]);
+            const float f_old = __builtin_amdgcn_exp2f(mx - mn);          // 0 while mx = -inf
+            const float f_new = __builtin_amdgcn_exp2f(ml[u][0] - mn);
+            lsum = lsum * f_old + f_new * ml[u][1];
+            o = o * f_old + f_new * ov[u];
+            mx = mn;
+        }
+    }
+    const float inv = 1.0f / lsum;
+    const int64_t off = qh * a.D + d;                      // [seq][heads][D]
+    if (a.o_dtype == MVLM_F32)
+        *reinterpret_cast<f32x4*>((float*)a.O + off) = o * inv;
+    else
+        *reinterpret_cast<u32x2*>((uint16_t*)a.O + off) =
+            u32x2{pack_f16x2(o[0] * inv, o[1] * inv), pack_f16x2(o[2] * inv, o[3] * inv)};
 }
 
 template <int KS, int DT, int NW>
@@ -320,9 +406,33 @@ static hipError_t launch_variant(hipStream_t s, const AttnArgs& a) {
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    const dim3 grid((unsigned)((a.seq_q + 31) / 32), (unsigned)a.heads);
-    launch_kernel(kernel, grid, dim3(64 * NW), (uint32_t)lds, s, a);
+    const dim3 grid((unsigned)((a.seq_q + 31) / 32), (unsigned)a.heads, (unsigned)a.splits);
+    if (a.splits == 1) {
+        launch_kernel(kernel, grid, dim3(64 * NW), (uint32_t)lds, s, a);
+        return hipGetLastError();
+    }
+    launch_kernel_part(LaunchPart::First, kernel, grid, dim3(64 * NW), (uint32_t)lds, s, a);
+    const int64_t items = (int64_t)a.seq_q * a.heads * (a.D / 4);
+    launch_kernel_part(LaunchPart::Last, attention_combine_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256),
+                       0, s, a);
     return hipGetLastError();
+}
+
+// Splits over keys: none when the (32-query tile, head) blocks alone cover the
+// CUs; otherwise enough for about two blocks per CU, keeping at least two key
+// tiles per split.
+static int pick_splits(int seq_q, int seq_kv, int heads, int num_cus) {
+    const int64_t blocks = (int64_t)(seq_q + 31) / 32 * heads;
+    const int tiles = (seq_kv + 31) / 32;
+    if (blocks >= num_cus || tiles < 4) return 1;
+    const int64_t want = (2 * (int64_t)num_cus + blocks - 1) / blocks;
+    return (int)std::max<int64_t>(1, std::min<int64_t>({want, tiles / 2, 64}));
+}
+
+size_t attention_workspace_bytes(int seq_q, int seq_kv, int heads, int head_dim, int num_cus) {
+    const int splits = pick_splits(seq_q, seq_kv, heads, num_cus);
+    if (splits == 1) return 0;
+    return (size_t)splits * seq_q * heads * (head_dim + 2) * sizeof(float);
 }
 
 // Waves per block: the fewest block rounds times key tiles per wave, with
@@ -348,10 +458,17 @@ static int pick_waves(int blocks, int key_tiles, int num_cus) {
     return best;
 }
 
+// MVLM_ATTN_WAVES=<1|2|4|8|16> forces the waves per block (tuning runs; read at
+// every launch).
 template <int KS, int DT>
 static hipError_t launch_dims(hipStream_t s, const AttnArgs& a, int num_cus) {
-    const int blocks = (a.seq_q + 31) / 32 * a.heads;
-    const int nw = pick_waves<KS, DT>(blocks, (a.seq_kv + 31) / 32, num_cus);
+    const int blocks = (a.seq_q + 31) / 32 * a.heads * a.splits;
+    int nw = pick_waves<KS, DT>(blocks, a.tiles_per_split, num_cus);
+    const char* force = std::getenv("MVLM_ATTN_WAVES");
+    if (force) {
+        const int f = std::atoi(force);
+        if ((f == 1 || f == 2 || f == 4 || f == 8 || f == 16) && f * AttnLayout<KS, DT>::REGION <= ATTN_LDS_MAX) nw = f;
+    }
     switch (nw) {
         case 1: return launch_variant<KS, DT, 1>(s, a);
         case 2: return launch_variant<KS, DT, 2>(s, a);
@@ -364,8 +481,14 @@ static hipError_t launch_dims(hipStream_t s, const AttnArgs& a, int num_cus) {
 }
 
 hipError_t launch_attention(hipStream_t s, const void* Q, const void* K, const void* V, void* O, int o_dtype,
-                            int seq_q, int seq_kv, int heads, int head_dim, int causal, float scale, int num_cus) {
+                            int seq_q, int seq_kv, int heads, int head_dim, int causal, float scale, int num_cus,
+                            void* workspace) {
     AttnArgs a{};
+    a.splits = pick_splits(seq_q, seq_kv, heads, num_cus);
+    const int tiles = (seq_kv + 31) / 32;
+    a.tiles_per_split = (tiles + a.splits - 1) / a.splits;
+    a.ws = (float*)workspace;
+    if (a.splits > 1 && !workspace) return hipErrorInvalidValue;
     a.Q = (const uint16_t*)Q; a.K = (const uint16_t*)K; a.V = (const uint16_t*)V; a.O = O;
     a.o_dtype = o_dtype;
     a.seq_q = seq_q; a.seq_kv = seq_kv; a.heads = heads; a.D = head_dim;

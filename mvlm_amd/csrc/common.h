@@ -7,6 +7,7 @@
 #include <hip/hip_bf16.h>
 
 #include <utility>
+#include <vector>
 
 #include <cstdarg>
 #include <cstdint>
@@ -19,6 +20,13 @@ struct mvlm_device {
     int ordinal = 0;
     hipStream_t stream = nullptr;
     hipDeviceProp_t prop{};
+    // Workspace for ops that hand partial results between two launches (split
+    // attention).  Grow-only: a larger request allocates a new block and keeps
+    // the old ones, so a pointer an op (or a captured graph) holds stays valid
+    // until the device is destroyed.  Ops on the device's one stream run in
+    // order, so they share the current block.
+    std::vector<void*> scratch_blocks;
+    size_t scratch_bytes = 0;
 };
 
 struct mvlm_buffer {
@@ -89,6 +97,9 @@ inline bool is_dense(int dt) { return dt == MVLM_F32 || dt == MVLM_F16 || dt == 
 inline bool is_quant(int dt) { return dt == MVLM_Q8_0 || dt == MVLM_Q4_0; }
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
+// Device workspace of at least `bytes` (see mvlm_device::scratch_blocks).
+int device_scratch(mvlm_device* dev, size_t bytes, void** out);
+
 // Launch bracketing: records the start marker when the caller asked for an
 // event, and finishes (end marker + hand-over) after the launch.
 struct LaunchScope {
@@ -116,6 +127,21 @@ inline void launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint3
     KernelTiming& t = kernel_timing();
     if (t.start)
         hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, t.start, t.stop, 0, std::forward<Args>(args)...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, shmem, s, std::forward<Args>(args)...);
+}
+
+// An op made of two dependent kernels: the first carries the start event and
+// the second the stop event, so plan profiling times the pair.
+enum class LaunchPart { First, Last };
+template <typename... KArgs, typename... Args>
+inline void launch_kernel_part(LaunchPart part, void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t shmem,
+                               hipStream_t s, Args&&... args) {
+    KernelTiming& t = kernel_timing();
+    hipEvent_t start = part == LaunchPart::First ? t.start : nullptr;
+    hipEvent_t stop = part == LaunchPart::Last ? t.stop : nullptr;
+    if (t.start)
+        hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, start, stop, 0, std::forward<Args>(args)...);
     else
         hipLaunchKernelGGL(kernel, grid, block, shmem, s, std::forward<Args>(args)...);
 }
@@ -155,9 +181,12 @@ hipError_t launch_gemm_mfma(hipStream_t s, const void* A, int ab_dtype, const vo
                             int c_dtype, int batch, int M, int N, int K, int64_t lda, int64_t ldb,
                             int64_t ldc, int64_t strideA, int64_t strideB, int64_t strideC,
                             int kread_b, int num_cus, const Epilogue* ep = nullptr);
-// fused attention, fp16 Q/K/V [seq][heads][head_dim], head_dim a multiple of 8 up to 128
+// fused attention, fp16 Q/K/V [seq][heads][head_dim], head_dim a multiple of 8 up to 128;
+// `workspace` holds attention_workspace_bytes(...) bytes (none when that is 0)
+size_t attention_workspace_bytes(int seq_q, int seq_kv, int heads, int head_dim, int num_cus);
 hipError_t launch_attention(hipStream_t s, const void* Q, const void* K, const void* V, void* O, int o_dtype,
-                            int seq_q, int seq_kv, int heads, int head_dim, int causal, float scale, int num_cus);
+                            int seq_q, int seq_kv, int heads, int head_dim, int causal, float scale, int num_cus,
+                            void* workspace);
 // row-wise argmax (first index of the largest key), one workgroup per row
 hipError_t launch_argmax(hipStream_t s, const void* x, int dtype, int rows, int n, int64_t ld, int* out);
 hipError_t launch_pack(hipStream_t s, const void* src, int dtype, int layout, int N, int K,

@@ -128,9 +128,35 @@ extern "C" int mvlm_device_destroy(mvlm_device* dev) {
         int st2 = check_hip(hipStreamDestroy(dev->stream), "hipStreamDestroy");
         if (st == MVLM_OK) st = st2;
     }
+    for (void* p : dev->scratch_blocks) (void)hipFree(p);
     delete dev;
     return st;
 }
+
+namespace mvlm {
+int device_scratch(mvlm_device* dev, size_t bytes, void** out) {
+    *out = nullptr;
+    if (bytes == 0) return MVLM_OK;
+    if (bytes > dev->scratch_bytes) {
+        HIP_TRY(hipSetDevice(dev->ordinal));
+        const size_t want = (bytes + 0xFFFFF) & ~(size_t)0xFFFFF;      // whole MiB
+        void* p = nullptr;
+        if (hipMalloc(&p, want) != hipSuccess || !p) {
+            (void)hipGetLastError();
+            return set_error(MVLM_ERR_OUT_OF_MEMORY, "workspace allocation of %zu bytes failed", want);
+        }
+        try {
+            dev->scratch_blocks.push_back(p);
+        } catch (...) {
+            (void)hipFree(p);
+            return set_error(MVLM_ERR_OUT_OF_MEMORY, "workspace bookkeeping failed");
+        }
+        dev->scratch_bytes = want;
+    }
+    *out = dev->scratch_blocks.back();
+    return MVLM_OK;
+}
+}  // namespace mvlm
 
 extern "C" int mvlm_device_get_info(const mvlm_device* dev, mvlm_device_info* info) {
     REQUIRE(dev && info, "mvlm_device_get_info: null argument");

@@ -94,6 +94,15 @@ def test_attention_long_cache_decode(dev, orc):
     run(dev, orc, 4, 2048, 32, 64, True, F32, seed=10)
 
 
+@pytest.mark.parametrize("waves", ["1", "2", "16"])
+def test_attention_forced_waves_with_key_splits(dev, orc, monkeypatch, waves):
+    """few (query tile, head) blocks: the keys are split over workgroups and
+    merged by a second kernel; every waves-per-block variant must agree"""
+    monkeypatch.setenv("MVLM_ATTN_WAVES", waves)
+    run(dev, orc, 1, 700, 8, 64, False, F32, seed=41)
+    run(dev, orc, 40, 300, 4, 72, True, F16, seed=42)
+
+
 def test_prefill_and_decode_entry_points(dev, orc):
     """the reference's dispatchers: prefill = causal, seq_q == seq_kv, fp16 out;
     decode = one query, no mask, fp16 out; both bit-identical to mvlm_attention"""
