@@ -87,8 +87,11 @@ __device__ __forceinline__ f32x16 mfma_f16(u32x4 a, u32x4 b, f32x16 c) {
                                                   0, 0, 0);
 }
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// two fp32 values to packed fp16, round to nearest even (one v_cvt_pk_f16_f32)
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
-    return (uint32_t)__half_as_ushort(__float2half(lo)) | ((uint32_t)__half_as_ushort(__float2half(hi)) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
 }
 
 template <int KS, int DT, int NW>
@@ -109,11 +112,10 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(const AttnArgs a) {
     uint16_t* ks = (uint16_t*)region;                     // [32 keys][KROW]
     uint16_t* vt = (uint16_t*)(region + 32 * L::KROW * 2);   // [32 DT dims][VROW]
 
-    // zero the K tile's padding columns D .. 16 KS once (contracted with Q's zeros)
-    for (int i = lane; i < 32 * (16 * KS - D); i += 64) {
-        const int key = i / (16 * KS - D), d = D + i % (16 * KS - D);
-        ks[key * L::KROW + d] = 0;
-    }
+    // zero the K tile's padding columns D .. 16 KS once (contracted with Q's
+    // zeros): D is a multiple of 8, so whole 16-byte chunks, one row per lane
+    if (lane < 32)
+        for (int d = D; d < 16 * KS; d += 8) *reinterpret_cast<u32x4*>(ks + lane * L::KROW + d) = u32x4{0u, 0u, 0u, 0u};
 
     // Raw buffer loads: an offset at or past num_records reads zeros, which
     // covers keys past seq_kv, queries past seq_q and the idle lanes of a
@@ -140,12 +142,18 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(const AttnArgs a) {
     int kv_end = a.seq_kv;
     if (a.causal) kv_end = min(a.seq_kv, min(qb0 + 32, a.seq_q) + shift);
 
-    // lane chunk c = lane + 64 i: keys 4 (c % 8) .. +3, dims 8 (c / 8) .. +7
+    // lane chunk c = lane + 64 i (c < D): keys 4 (c / cpr) .. +3, dims 8 (c % cpr) .. +7
+    // with cpr = D / 8 chunks per row; consecutive lanes take consecutive
+    // 16-byte chunks of one row, so each quad of lanes reads one 64-byte run
+    const int cpr = D / 8;
     uint32_t coff[VI];
+    int ckey[VI], cdim[VI];
 #pragma unroll
     for (int i = 0; i < VI; ++i) {
         const int c = lane + 64 * i;
-        coff[i] = c < D ? (uint32_t)(4 * (c & 7) * row2 + (head * D + 8 * (c >> 3)) * 2) : OOB;
+        ckey[i] = 4 * (c / cpr);
+        cdim[i] = 8 * (c % cpr);
+        coff[i] = c < D ? (uint32_t)(ckey[i] * row2 + (head * D + cdim[i]) * 2) : OOB;
     }
     u32x4 tk[VI][4], tv[VI][4];
     auto load_tile = [&](int kv0) {
@@ -164,15 +172,17 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(const AttnArgs a) {
         for (int i = 0; i < VI; ++i) {
             const int c = lane + 64 * i;
             if (64 * i + 64 <= D || c < D) {
-                const int key0 = 4 * (c & 7), d = 8 * (c >> 3);
+                const int key0 = ckey[i], d = cdim[i];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) *reinterpret_cast<u32x4*>(ks + (key0 + u) * L::KROW + d) = tk[i][u];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     // dim d + j of keys key0 .. key0+3
-                    const int sh = 16 * (j & 1);
-                    const uint32_t k01 = ((tv[i][0][j >> 1] >> sh) & 0xFFFFu) | (((tv[i][1][j >> 1] >> sh) & 0xFFFFu) << 16);
-                    const uint32_t k23 = ((tv[i][2][j >> 1] >> sh) & 0xFFFFu) | (((tv[i][3][j >> 1] >> sh) & 0xFFFFu) << 16);
+                    // v_perm_b32 picks bytes of {src0 (4..7), src1 (0..3)}: the low
+                    // halves (j even, selector 0x05040100) or the high halves (0x07060302)
+                    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+                    const uint32_t k01 = __builtin_amdgcn_perm(tv[i][1][j >> 1], tv[i][0][j >> 1], sel);
+                    const uint32_t k23 = __builtin_amdgcn_perm(tv[i][3][j >> 1], tv[i][2][j >> 1], sel);
                     *reinterpret_cast<u32x2*>(vt + (d + j) * L::VROW + key0) = u32x2{k01, k23};
                 }
             }
@@ -208,20 +218,18 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(const AttnArgs a) {
             const u32x4 kf = *reinterpret_cast<const u32x4*>(ks + l32 * L::KROW + 16 * st + 8 * h);
             s = mfma_f16(kf, qf[st], s);
         }
-        if (kv0 + 32 <= open_end) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) s[r] *= a.scale_log2;
-        } else {
+        // raw dot products; the scale (> 0) is applied inside the exponent
+        if (kv0 + 32 > open_end) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int key = kv0 + 8 * (r >> 2) + 4 * h + (r & 3);
-                s[r] = key > last_key ? -INFINITY : s[r] * a.scale_log2;
+                if (key > last_key) s[r] = -INFINITY;
             }
         }
         float tmax = s[0];
 #pragma unroll
         for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, s[r]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * a.scale_log2;
         // Lazy rescaling: the reference point mrun moves only when a score
         // exceeds it by more than 8 (probabilities stay <= 2^8, exact range
         // for fp16), so most tiles skip the accumulator rescale.
@@ -242,7 +250,7 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(const AttnArgs a) {
         float p[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            p[r] = __builtin_amdgcn_exp2f(s[r] - msafe);
+            p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], a.scale_log2, -msafe));
             psum += p[r];
         }
         psum += __shfl_xor(psum, 32, 64);
