@@ -361,10 +361,11 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(const AttnArgs a) {
 }
 
 // Merges the splits' partial softmaxes: thread = (query, head, 4 dims).  The
-// records are read 8 at a time (all loads in flight together) and folded in
-// with an online rescale, so no pass over the maxima comes first.
+// records are read 16 at a time (all loads in flight together; the split
+// count is at most 32) and folded in with an online rescale, so no pass over
+// the maxima comes first.
 __global__ __launch_bounds__(256) void attention_combine_kernel(const AttnArgs a) {
-    constexpr int BATCH = 8;
+    constexpr int BATCH = 16;
     const int64_t item = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int d4 = a.D / 4;
     if (item >= (int64_t)a.seq_q * a.heads * d4) return;
@@ -434,7 +435,7 @@ static int pick_splits(int seq_q, int seq_kv, int heads, int num_cus) {
     const int tiles = (seq_kv + 31) / 32;
     if (blocks >= num_cus || tiles < 4) return 1;
     const int64_t want = (2 * (int64_t)num_cus + blocks - 1) / blocks;
-    return (int)std::max<int64_t>(1, std::min<int64_t>({want, tiles / 2, 64}));
+    return (int)std::max<int64_t>(1, std::min<int64_t>({want, tiles / 2, 32}));
 }
 
 size_t attention_workspace_bytes(int seq_q, int seq_kv, int heads, int head_dim, int num_cus) {
