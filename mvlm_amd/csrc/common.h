@@ -177,10 +177,13 @@ hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const*
                                     const mvlm_weight* const* ws, void* const* ys, const int* y_dtypes, int num_cus,
                                     const Epilogue* eps = nullptr);
 inline int64_t weight_row_bytes(const mvlm_weight* w) { return is_dense(w->dtype) ? w->ld * (int64_t)dtype_size(w->dtype) : w->ld; }
+// MFMA GEMM; a K split (chosen by the launcher's cost model) needs
+// gemm_workspace_bytes(...) bytes of workspace
+size_t gemm_workspace_bytes(int batch, int M, int N, int K, int num_cus);
 hipError_t launch_gemm_mfma(hipStream_t s, const void* A, int ab_dtype, const void* B, void* C,
                             int c_dtype, int batch, int M, int N, int K, int64_t lda, int64_t ldb,
                             int64_t ldc, int64_t strideA, int64_t strideB, int64_t strideC,
-                            int kread_b, int num_cus, const Epilogue* ep = nullptr);
+                            int kread_b, int num_cus, const Epilogue* ep, void* workspace, size_t workspace_bytes);
 // fused attention, fp16 Q/K/V [seq][heads][head_dim], head_dim a multiple of 8 up to 128;
 // `workspace` holds attention_workspace_bytes(...) bytes (none when that is 0)
 size_t attention_workspace_bytes(int seq_q, int seq_kv, int heads, int head_dim, int num_cus);

@@ -39,8 +39,17 @@
 
 namespace mvlm {
 
-constexpr int BK = 64;       // K per stage
-constexpr int ROWH = BK;     // elements per LDS row (128 bytes)
+// LDS geometry of a stage BK elements wide: one row per operand row, RB bytes
+// (LPR 16-byte slots); one direct-load instruction fills RPI rows (1 KiB).
+// Slot s of row r is stored at s ^ swz(r): a ds_read_b128 phase (16 lanes,
+// 16 consecutive rows, one logical slot) then hits 16 distinct 16-byte bank
+// groups of the 256-byte bank period (two 128-byte rows, or four 64-byte rows).
+template <int BK>
+struct StageGeom {
+    static_assert(BK == 32 || BK == 64, "stage width");
+    static constexpr int ROWH = BK, RB = 2 * BK, LPR = RB / 16, RPI = 1024 / RB;
+    __device__ static __forceinline__ int swz(int r) { return BK == 64 ? (r >> 1) & 7 : (r >> 2) & 3; }
+};
 
 struct GemmArgs {
     const uint16_t* A;
@@ -53,6 +62,12 @@ struct GemmArgs {
     int tiles_m, tiles_n;
     Epilogue ep;        // applied when ep_on (mul / res indexed like C)
     int ep_on;
+    // split-K: grid z = batch * splits; split s covers K stages
+    // [s * split_stages, (s + 1) * split_stages) and, when splits > 1, writes
+    // its fp32 partial to ws[(b * splits + s) * M * N + m * N + n] for
+    // gemm_splitk_reduce_kernel (which then applies the epilogue)
+    int splits, split_stages;
+    float* ws;
 };
 
 template <bool BF16>
@@ -64,46 +79,52 @@ __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
 }
 
 // Direct loads of one operand's stage: ROWS rows starting at tile row r0,
-// K columns [k0, k0+64).  Wave w of NW issues 8-row groups w, w+NW, ...
-template <int ROWS, int NW>
+// K columns [k0, k0+BK).  Wave w of NW issues RPI-row groups w, w+NW, ...;
+// lane i writes LDS bytes [16i, 16i+16) of its group, i.e. row RPI g + i/LPR,
+// physical slot i%LPR, and so fetches logical slot (i%LPR) ^ swz(row).
+template <int BK, int ROWS, int NW>
 __device__ __forceinline__ void stage_direct(const uint16_t* __restrict__ base, int64_t ld, int r0, int rmax, int k0,
                                              uint16_t* lds, int wave, int lane) {
-    // logical 16-byte slot this lane fetches: its LDS row is 8g + (lane >> 3)
-    // with g = wave + NW*t (NW even), so (row >> 1) & 7 = (4 * (wave & 1) + (lane >> 4)) & 7
-    const int ls = (lane & 7) ^ ((4 * (wave & 1) + (lane >> 4)) & 7);
-    static_assert((ROWS / 8) % NW == 0, "8-row groups must split evenly over the waves");
+    using G = StageGeom<BK>;
+    static_assert((ROWS / G::RPI) % NW == 0, "row groups must split evenly over the waves");
 #pragma unroll
-    for (int t = 0; t < ROWS / (8 * NW); ++t) {
+    for (int t = 0; t < ROWS / (G::RPI * NW); ++t) {
         const int g = wave + NW * t;
-        const int r = min(r0 + 8 * g + (lane >> 3), rmax);
+        const int lr = G::RPI * g + lane / G::LPR;
+        const int ls = (lane % G::LPR) ^ G::swz(lr);
+        const int r = min(r0 + lr, rmax);
         const uint16_t* src = base + (int64_t)r * ld + k0 + ls * 8;
-        asm_global_load_lds_b128(src, __builtin_amdgcn_readfirstlane(lds_offset(lds + 8 * g * ROWH)));
+        asm_global_load_lds_b128(src, __builtin_amdgcn_readfirstlane(lds_offset(lds + G::RPI * g * G::ROWH)));
     }
 }
 
 // Guarded loads of the last stage: 16-byte chunks at or beyond kread are zero.
-template <int ROWS, int NW>
+template <int BK, int ROWS, int NW>
 __device__ __forceinline__ void stage_guarded(const uint16_t* __restrict__ base, int64_t ld, int r0, int rmax, int k0,
                                               int kread, uint16_t* lds, int wave, int lane) {
-    const int ls = (lane & 7) ^ ((4 * (wave & 1) + (lane >> 4)) & 7);
-    static_assert((ROWS / 8) % NW == 0, "8-row groups must split evenly over the waves");
+    using G = StageGeom<BK>;
+    static_assert((ROWS / G::RPI) % NW == 0, "row groups must split evenly over the waves");
 #pragma unroll
-    for (int t = 0; t < ROWS / (8 * NW); ++t) {
+    for (int t = 0; t < ROWS / (G::RPI * NW); ++t) {
         const int g = wave + NW * t;
-        const int r = min(r0 + 8 * g + (lane >> 3), rmax);
+        const int lr = G::RPI * g + lane / G::LPR;
+        const int ls = (lane % G::LPR) ^ G::swz(lr);
+        const int r = min(r0 + lr, rmax);
         const int k = k0 + ls * 8;
         u32x4 v = {0, 0, 0, 0};
         if (k < kread) v = *reinterpret_cast<const u32x4*>(base + (int64_t)r * ld + k);
-        *reinterpret_cast<u32x4*>(lds + 8 * g * ROWH + lane * 8) = v;
+        *reinterpret_cast<u32x4*>(lds + G::RPI * g * G::ROWH + lane * 8) = v;
     }
 }
 
-template <bool BF16, int BM, int BN, int STAGES, int WGM, int WGN>
+template <bool BF16, int BM, int BN, int BK, int STAGES, int WGM, int WGN>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(const GemmArgs p) {
+    using G = StageGeom<BK>;
+    constexpr int ROWH = G::ROWH;
     constexpr int NW = WGM * WGN;                // waves per block (WGM x WGN grid)
     constexpr int WM = BM / WGM, WN = BN / WGN;  // wave sub-tile
     constexpr int TM = WM / 32, TN = WN / 32;    // 32x32 MFMA tiles per wave
-    constexpr int LA = (BM / 8 + BN / 8) / NW;   // direct-load instructions per wave per stage
+    constexpr int LA = (BM + BN) / G::RPI / NW;  // direct-load instructions per wave per stage
     constexpr int SLOT = (BM + BN) * ROWH;       // elements per ring slot
     static_assert(TM + TN <= 15, "fragment reads must fit the lgkmcnt field");
     __shared__ __attribute__((aligned(1024))) uint16_t smem[STAGES * SLOT];
@@ -118,25 +139,29 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(const GemmArg
     const int tm = t % p.tiles_m, tn = t / p.tiles_m;
     const int m0 = tm * BM, n0 = tn * BN;
 
-    const uint16_t* __restrict__ A = p.A + (int64_t)blockIdx.z * p.sA;
-    const uint16_t* __restrict__ B = p.B + (int64_t)blockIdx.z * p.sB;
+    const int batch = blockIdx.z / p.splits, split = blockIdx.z % p.splits;
+    const uint16_t* __restrict__ A = p.A + (int64_t)batch * p.sA;
+    const uint16_t* __restrict__ B = p.B + (int64_t)batch * p.sB;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
     const int K = p.K;
-    const int nk = (K + BK - 1) / BK;
-    // the last stage needs the guarded path when it reaches past K (A) or past
-    // B's zero-padded width
-    const bool tail_a = (nk * BK > K);
-    const bool tail_b = (nk * BK > p.kread_b);
+    const int nk_all = (K + BK - 1) / BK;
+    const int kt0 = split * p.split_stages;                     // this split's first stage
+    const int nk = min(nk_all - kt0, p.split_stages);           // stages of this split (>= 1)
+    // the global last stage needs the guarded path when it reaches past K (A)
+    // or past B's zero-padded width
+    const bool tail_a = (nk_all * BK > K) && kt0 + nk == nk_all;
+    const bool tail_b = (nk_all * BK > p.kread_b) && kt0 + nk == nk_all;
 
     auto issue = [&](int kt) {
         uint16_t* slot = smem + (kt % STAGES) * SLOT;
-        const int k0 = kt * BK;
+        const int k0 = (kt0 + kt) * BK;
         const bool last = (kt == nk - 1);
-        if (last && tail_a) stage_guarded<BM, NW>(A, p.lda, m0, p.M - 1, k0, K, slot, wave, lane);
-        else stage_direct<BM, NW>(A, p.lda, m0, p.M - 1, k0, slot, wave, lane);
-        if (last && tail_b) stage_guarded<BN, NW>(B, p.ldb, n0, p.N - 1, k0, p.kread_b, slot + BM * ROWH, wave, lane);
-        else stage_direct<BN, NW>(B, p.ldb, n0, p.N - 1, k0, slot + BM * ROWH, wave, lane);
+        if (last && tail_a) stage_guarded<BK, BM, NW>(A, p.lda, m0, p.M - 1, k0, K, slot, wave, lane);
+        else stage_direct<BK, BM, NW>(A, p.lda, m0, p.M - 1, k0, slot, wave, lane);
+        if (last && tail_b)
+            stage_guarded<BK, BN, NW>(B, p.ldb, n0, p.N - 1, k0, p.kread_b, slot + BM * ROWH, wave, lane);
+        else stage_direct<BK, BN, NW>(B, p.ldb, n0, p.N - 1, k0, slot + BM * ROWH, wave, lane);
     };
 
     f32x16 acc[TM][TN];
@@ -152,12 +177,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(const GemmArg
     // compiler's own waits would put vmcnt(0) before every read (the ring is
     // filled by direct loads) and merge the loop-carried reads into
     // lgkmcnt(0).  Row r of a fragment is lane&31 plus a multiple of 32, so its
-    // swizzle (r >> 1) & 7 is the lane's; byte offsets: row * 128 + slot * 16.
+    // swizzle is the lane's; byte offsets: row * RB + slot * 16.
     struct Frags { u32x4 a[TM]; u32x4 b[TN]; };
     const uint32_t lds0 = lds_offset(smem);
     const uint32_t a_lane = (uint32_t)((wm * WM + (lane & 31)) * ROWH * 2);
     const uint32_t b_lane = (uint32_t)((BM + wn * WN + (lane & 31)) * ROWH * 2);
-    const int swz = (lane >> 1) & 7, half = lane >> 5;
+    const int swz = G::swz(lane & 31), half = lane >> 5;
     auto load_frags = [&](int slot_idx, int ks, Frags& f) {
         const uint32_t base = lds0 + (uint32_t)(slot_idx * SLOT * 2) + (uint32_t)((((2 * ks + half) ^ swz)) << 4);
 #pragma unroll
@@ -209,7 +234,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(const GemmArg
     // next stage's first fragments, so neither the barrier nor that read sits
     // in front of an idle matrix core.  Stage kt+1 was issued STAGES-1
     // iterations before it is waited for.
-    // Two fragment sets alternate by k-step parity (BK/16 = 4 k-steps per
+    // Two fragment sets alternate by k-step parity (BK/16 = 4 or 2 k-steps per
     // stage, so a stage always starts on set 0); with the k-step loop unrolled
     // they are distinct registers and no copies are needed.
     Frags f[2];
@@ -234,7 +259,23 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(const GemmArg
         }
     }
 
-    const int64_t c_off = (int64_t)blockIdx.z * p.sC;
+    if (p.splits > 1) {   // fp32 partial for the reduce kernel
+        float* ws = p.ws + (int64_t)blockIdx.z * p.M * p.N;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int col = n0 + wn * WN + j * 32 + (lane & 31);
+                if (col >= p.N) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    if (row < p.M) ws[(int64_t)row * p.N + col] = acc[i][j][r];
+                }
+            }
+        return;
+    }
+    const int64_t c_off = (int64_t)batch * p.sC;
     if (!p.ep_on) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
@@ -267,60 +308,106 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(const GemmArg
     }
 }
 
+// Sums the split-K partials in split order (deterministic), applies the
+// epilogue and stores C: thread = one output element.
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const GemmArgs p) {
+    const int64_t mn = (int64_t)p.M * p.N;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int b = blockIdx.y;
+    if (i >= mn) return;
+    const float* ws = p.ws + (int64_t)b * p.splits * mn + i;
+    float v = 0.0f;
+    for (int s = 0; s < p.splits; ++s) v += ws[s * mn];
+    const int row = (int)(i / p.N), col = (int)(i - (int64_t)row * p.N);
+    const int64_t idx = (int64_t)b * p.sC + (int64_t)row * p.ldc + col;
+    store_out(p.C, idx, p.ep_on ? apply_epilogue(p.ep, v, idx, col) : v, p.c_dtype);
+}
+
 // ---- launch configuration ----------------------------------------------------
 
 typedef void (*GemmKernel)(const GemmArgs);
 
 struct TileCfg {
-    int bm, bn, stages, waves;
+    int bm, bn, bk, stages, waves;
     int per_cu;       // resident blocks per CU (LDS ring and registers)
     int eff;          // TFLOP/s of a full-wave 4096^3 fp16 run (selection weight)
     GemmKernel f16, bf16;
 };
 
-#define MVLM_TILE(BMv, BNv, Sv, WMv, WNv, PER_CU, EFF)                                             \
-    TileCfg{BMv, BNv, Sv, WMv * WNv, PER_CU, EFF, gemm_mfma_kernel<false, BMv, BNv, Sv, WMv, WNv>, \
-            gemm_mfma_kernel<true, BMv, BNv, Sv, WMv, WNv>}
-// The first four are the automatic choices; the others are kept for tuning.
+#define MVLM_TILE(BMv, BNv, BKv, Sv, WMv, WNv, PER_CU, EFF)                                          \
+    TileCfg{BMv, BNv, BKv, Sv, WMv * WNv, PER_CU, EFF, gemm_mfma_kernel<false, BMv, BNv, BKv, Sv, WMv, WNv>, \
+            gemm_mfma_kernel<true, BMv, BNv, BKv, Sv, WMv, WNv>}
+// The first five are the automatic choices (eff measured at 4096^3, fp16 in,
+// fp32 out); the others are kept for tuning.
 static const TileCfg kTiles[] = {
-    MVLM_TILE(256, 256, 2, 4, 2, 1, 831), MVLM_TILE(256, 128, 2, 4, 2, 1, 714),
-    MVLM_TILE(128, 128, 4, 4, 2, 1, 537), MVLM_TILE(64, 64, 4, 2, 2, 2, 386),
-    MVLM_TILE(256, 128, 3, 4, 2, 1, 628), MVLM_TILE(128, 128, 4, 2, 2, 1, 502),
-    MVLM_TILE(128, 64, 4, 2, 2, 1, 375),
+    MVLM_TILE(256, 256, 64, 2, 4, 2, 1, 907), MVLM_TILE(256, 128, 64, 2, 4, 2, 1, 785),
+    MVLM_TILE(192, 128, 64, 3, 2, 4, 1, 636), MVLM_TILE(128, 128, 64, 4, 4, 2, 1, 619),
+    MVLM_TILE(64, 64, 64, 4, 2, 2, 2, 401),
+    MVLM_TILE(256, 128, 64, 3, 4, 2, 1, 628), MVLM_TILE(128, 128, 64, 4, 2, 2, 1, 502),
+    MVLM_TILE(128, 64, 64, 4, 2, 2, 1, 375),
+    MVLM_TILE(256, 256, 32, 4, 4, 2, 1, 849), MVLM_TILE(256, 256, 32, 5, 4, 2, 1, 828),
+    MVLM_TILE(256, 128, 32, 6, 4, 2, 1, 686), MVLM_TILE(128, 128, 32, 8, 4, 2, 1, 541),
+    MVLM_TILE(128, 128, 32, 4, 4, 2, 2, 689), MVLM_TILE(192, 128, 32, 6, 2, 2, 1, 460),
 };
-constexpr int kAutoTiles = 4;
+constexpr int kAutoTiles = 5;
 #undef MVLM_TILE
 
-// The tile with the best (full-wave throughput x fraction of the last round
-// of blocks that is busy x fraction of computed outputs that are stored).
-// MVLM_GEMM_TILE=<bm>x<bn>s<stages>w<waves> forces a compiled tile (tuning runs).
-static const TileCfg& pick_tile(int M, int N, int batch, int num_cus) {
-    static const char* force = std::getenv("MVLM_GEMM_TILE");
+struct GemmPlan {
+    const TileCfg* tile;
+    int splits, split_stages;
+};
+
+// The tile and K split with the least modelled time: block rounds x one
+// block's share of the tile's full-chip throughput (eff, all slots busy),
+// plus, for a split, writing and re-reading the fp32 partials (~4 TB/s) and a
+// second launch.  MVLM_GEMM_TILE=<bm>x<bn>s<stages>w<waves>[k<bk>] forces a
+// compiled tile and MVLM_GEMM_SPLITS=<n> a split count (tuning runs; read at
+// every launch).
+static GemmPlan plan_gemm(int M, int N, int K, int batch, int num_cus) {
+    GemmPlan best{&kTiles[kAutoTiles - 1], 1, 0};
+    double best_t = 1e30;
+    const char* force = std::getenv("MVLM_GEMM_TILE");
+    const TileCfg* forced = nullptr;
     if (force) {
-        int bm = 0, bn = 0, st = 0, w = 0;
-        if (std::sscanf(force, "%dx%ds%dw%d", &bm, &bn, &st, &w) == 4)
+        int bm = 0, bn = 0, st = 0, w = 0, bk = 64;
+        if (std::sscanf(force, "%dx%ds%dw%dk%d", &bm, &bn, &st, &w, &bk) >= 4)
             for (const TileCfg& c : kTiles)
-                if (c.bm == bm && c.bn == bn && c.stages == st && c.waves == w) return c;
+                if (c.bm == bm && c.bn == bn && c.stages == st && c.waves == w && c.bk == bk) forced = &c;
     }
-    const TileCfg* best = &kTiles[kAutoTiles - 1];
-    double best_score = -1.0;
-    for (int i = 0; i < kAutoTiles; ++i) {
-        const TileCfg& c = kTiles[i];
-        const int64_t tiles = (int64_t)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * batch;
-        const int64_t slots = (int64_t)num_cus * c.per_cu;
-        const int64_t rounds = (tiles + slots - 1) / slots;
-        const double fill = (double)tiles / (double)(rounds * slots);
-        const double useful = (double)M * N * batch / (double)(tiles * c.bm * c.bn);
-        const double score = c.eff * fill * useful;
-        if (score > best_score) { best_score = score; best = &c; }
+    const char* fs = std::getenv("MVLM_GEMM_SPLITS");
+    const int forced_splits = fs ? std::atoi(fs) : 0;
+    const int n_cand = forced ? 1 : kAutoTiles;
+    for (int i = 0; i < n_cand; ++i) {
+        const TileCfg& c = forced ? *forced : kTiles[i];
+        const int nk = (K + c.bk - 1) / c.bk;
+        for (int splits : {1, 2, 3, 4, 6, 8}) {
+            if (forced_splits > 0 && splits != forced_splits) continue;
+            if (splits > 1 && nk < 4 * splits) break;                 // keep at least 4 stages per split
+            const int ss = (nk + splits - 1) / splits;
+            const int used = (nk + ss - 1) / ss;                         // non-empty splits
+            if (used != splits) continue;
+            const int64_t tiles = (int64_t)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * batch * splits;
+            const int64_t slots = (int64_t)num_cus * c.per_cu;
+            const int64_t rounds = (tiles + slots - 1) / slots;
+            const double block_flops = 2.0 * c.bm * c.bn * (double)ss * c.bk;
+            double t = rounds * block_flops / (c.eff * 1e12 / (double)slots);
+            if (splits > 1) t += (double)M * N * batch * 4.0 * (2.0 * splits + 1.0) / 4e12 + 3e-6;
+            if (t < best_t) { best_t = t; best = GemmPlan{&c, splits, ss}; }
+        }
     }
-    return *best;
+    if (best.split_stages == 0) best.split_stages = (K + best.tile->bk - 1) / best.tile->bk;
+    return best;
+}
+
+size_t gemm_workspace_bytes(int batch, int M, int N, int K, int num_cus) {
+    const GemmPlan g = plan_gemm(M, N, K, batch, num_cus > 0 ? num_cus : 256);
+    return g.splits > 1 ? (size_t)g.splits * batch * M * N * sizeof(float) : 0;
 }
 
 hipError_t launch_gemm_mfma(hipStream_t s, const void* A, int ab_dtype, const void* B, void* C, int c_dtype,
                             int batch, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
                             int64_t strideA, int64_t strideB, int64_t strideC, int kread_b, int num_cus,
-                            const Epilogue* ep) {
+                            const Epilogue* ep, void* workspace, size_t workspace_bytes) {
     GemmArgs a{};
     a.A = (const uint16_t*)A; a.B = (const uint16_t*)B; a.C = C; a.c_dtype = c_dtype;
     a.M = M; a.N = N; a.K = K; a.lda = lda; a.ldb = ldb; a.ldc = ldc;
@@ -330,11 +417,25 @@ hipError_t launch_gemm_mfma(hipStream_t s, const void* A, int ab_dtype, const vo
         a.ep = *ep;
         a.ep_on = 1;
     }
-    const TileCfg& t = pick_tile(M, N, batch, num_cus > 0 ? num_cus : 256);
+    const GemmPlan g = plan_gemm(M, N, K, batch, num_cus > 0 ? num_cus : 256);
+    const TileCfg& t = *g.tile;
     a.tiles_m = (M + t.bm - 1) / t.bm;
     a.tiles_n = (N + t.bn - 1) / t.bn;
-    dim3 grid((unsigned)(a.tiles_m * a.tiles_n), 1, (unsigned)batch);
-    launch_kernel(ab_dtype == MVLM_BF16 ? t.bf16 : t.f16, grid, dim3(64 * t.waves), 0, s, a);
+    a.splits = g.splits;
+    a.split_stages = g.split_stages;
+    a.ws = (float*)workspace;
+    if (g.splits > 1 && (!workspace || workspace_bytes < (size_t)g.splits * batch * M * N * sizeof(float)))
+        return hipErrorInvalidValue;
+    dim3 grid((unsigned)(a.tiles_m * a.tiles_n), 1, (unsigned)(batch * g.splits));
+    GemmKernel k = ab_dtype == MVLM_BF16 ? t.bf16 : t.f16;
+    if (g.splits == 1) {
+        launch_kernel(k, grid, dim3(64 * t.waves), 0, s, a);
+        return hipGetLastError();
+    }
+    launch_kernel_part(LaunchPart::First, k, grid, dim3(64 * t.waves), 0, s, a);
+    const int64_t mn = (int64_t)M * N;
+    launch_kernel_part(LaunchPart::Last, gemm_splitk_reduce_kernel, dim3((unsigned)((mn + 255) / 256), (unsigned)batch),
+                       dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -40,7 +40,8 @@ struct Op {
     // attention: M = seq_q, N = seq_kv, batch = heads, K = head_dim
     int causal = 0;
     float scale = 0.0f;
-    void* workspace = nullptr;
+    void* workspace = nullptr;    // attention key splits, GEMM K splits
+    size_t workspace_bytes = 0;
 };
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -119,7 +120,8 @@ int make_gemm_packed(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, const 
     op->lda = K; op->ldb = W->ld; op->ldc = N;
     op->kread_b = (int)W->ld;     // packed rows are zero padded to ld = roundup(K, 64)
     op->num_cus = dev->prop.multiProcessorCount;
-    return MVLM_OK;
+    op->workspace_bytes = gemm_workspace_bytes(1, M, N, K, op->num_cus);
+    return device_scratch(dev, op->workspace_bytes, &op->workspace);
 }
 
 int make_gemm_batched(mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer* B, mvlm_buffer* C, int batch,
@@ -144,7 +146,8 @@ int make_gemm_batched(mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer*
     op->lda = lda; op->ldb = ldb; op->ldc = ldc; op->sA = sA; op->sB = sB; op->sC = sC;
     op->kread_b = K;
     op->num_cus = dev->prop.multiProcessorCount;
-    return MVLM_OK;
+    op->workspace_bytes = gemm_workspace_bytes(batch, M, N, K, op->num_cus);
+    return device_scratch(dev, op->workspace_bytes, &op->workspace);
 }
 
 int make_attention(mvlm_device* dev, const mvlm_buffer* Q, const mvlm_buffer* K, const mvlm_buffer* V,
@@ -272,7 +275,8 @@ hipError_t enqueue_op(hipStream_t s, const Op& op) {
             return launch_gemm_tiled(s, (const uint16_t*)op.a, (const uint16_t*)op.b, (uint16_t*)op.c, op.M, op.N, op.K);
         case OP_GEMM_MFMA:
             return launch_gemm_mfma(s, op.a, op.a_dtype, op.b, op.c, op.c_dtype, op.batch, op.M, op.N, op.K,
-                                    op.lda, op.ldb, op.ldc, op.sA, op.sB, op.sC, op.kread_b, op.num_cus, &op.ep);
+                                    op.lda, op.ldb, op.ldc, op.sA, op.sB, op.sC, op.kread_b, op.num_cus, &op.ep,
+                                    op.workspace, op.workspace_bytes);
         case OP_GEMV_DENSE:
             if (stream_supported(op.w))
                 return launch_gemv_stream(s, op.a, op.a_dtype, op.w, op.c, op.c_dtype, op.num_cus, &op.ep);

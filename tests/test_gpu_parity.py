@@ -454,3 +454,44 @@ def test_gemv_grouped_errors(dev):
         dev.gemv_grouped([(x, F32, Wlong, y, F32)])
     assert e.value.code == native.ERR_UNSUPPORTED
     dev.gemv(x, F32, Wlong, y, F32, 1, 65536)            # the single entry point still serves it
+
+
+@pytest.mark.parametrize("splits", ["2", "3", "4"])
+@pytest.mark.parametrize("M,N,K,ab,cd", [(129, 130, 1000, F16, BF16), (768, 256, 2048, F16, F32),
+                                         (33, 65, 1032, BF16, F16)])
+def test_gemm_forced_k_splits(dev, orc, monkeypatch, splits, M, N, K, ab, cd):
+    """K split over workgroups (fp32 partials in the device workspace, summed in
+    split order by a second kernel), including a K tail past the last full stage"""
+    monkeypatch.setenv("MVLM_GEMM_SPLITS", splits)
+    check_packed(dev, orc, M, N, K, ab, cd, seed=300 + int(splits))
+
+
+def test_gemm_k_splits_with_epilogue_and_batches(dev, orc, monkeypatch):
+    from test_gpu_epilogue import check as ep_check, make_operands
+    from mvlm_amd import native
+    monkeypatch.setenv("MVLM_GEMM_SPLITS", "3")
+    M, N, K = 96, 200, 1536
+    A = orc.normal_f16(M * K, 0x310)
+    Wt = orc.normal_f16(N * K, 0x311, 0.05)
+    W = dev.pack(Wt, F16, N, K)
+    ops, vals = make_operands(dev, orc, M, N, F32, 0x312, True, True, True)
+    C = ops["residual"]                                    # in-place residual add
+    dev.gemm_packed_ex(dev.upload(A), F16, W, C, F32, M, N, K, bias=ops["bias"], act=native.ACT_GELU_TANH,
+                       mul=ops["mul"], residual=C)
+    got = C.download(np.float32, M * N).astype(np.float64).reshape(M, N)
+    Y64, S = orc.gemm_f64(widen(orc, A, F16).reshape(M, K), widen(orc, Wt, F16).reshape(N, K), M, N, K)
+    ep_check(orc, got, Y64, S, vals, native.ACT_GELU_TANH, F32, 1e-4)
+    # batched Q K^T with splits: every head equals its own unsplit product within tolerance
+    H, Sq, D = 4, 100, 512
+    Q = orc.normal_f16(Sq * H * D, 0x313)
+    Kt = orc.normal_f16(Sq * H * D, 0x314)
+    dQ, dK, dC = dev.upload(Q), dev.upload(Kt), dev.alloc(H * Sq * Sq * 4)
+    dev.gemm_batched(dQ, dK, dC, H, Sq, Sq, D, H * D, H * D, Sq, D, D, Sq * Sq)
+    got = dC.download(np.float32).reshape(H, Sq, Sq)
+    for h in range(H):
+        q = Q.reshape(Sq, H, D)[:, h, :].copy()
+        k = Kt.reshape(Sq, H, D)[:, h, :].copy()
+        ref = orc.gemm_nk("f16", q, k, Sq, Sq, D)
+        _, Sc = orc.gemm_f64(orc.f16_to_f32(q).astype(np.float64), orc.f16_to_f32(k).astype(np.float64), Sq, Sq, D)
+        ok, worst = within(got[h], ref, Sc, 1e-3)
+        assert ok, (h, worst)
