@@ -169,8 +169,11 @@ hipError_t launch_gemv_dense(hipStream_t s, const void* x, int x_dtype, const mv
 // Q8_0 / Q4_0 skinny GEMM on the matrix cores, 1 <= M <= 16 (any row length)
 hipError_t launch_gemm_skinny(hipStream_t s, const float* X, const mvlm_weight* W, float* Y, int M, int N, int K,
                               int num_cus, const Epilogue* ep = nullptr);
-// M == 1 streaming GEMV for every weight format (rows of at most 16 KiB).
-bool stream_supported(const mvlm_weight* w);
+// M == 1 streaming GEMV for every weight format (rows of at most 16 KiB), and
+// for quantized weights 2 <= M <= 4 rows of x (launch_gemv_stream_batch).
+bool stream_supported(const mvlm_weight* w, int M = 1);
+hipError_t launch_gemv_stream_batch(hipStream_t s, const float* x, const mvlm_weight* W, float* y, int M,
+                                    int num_cus, const Epilogue* ep = nullptr);
 hipError_t launch_gemv_stream(hipStream_t s, const void* x, int x_dtype, const mvlm_weight* W, void* y,
                               int y_dtype, int num_cus, const Epilogue* ep = nullptr);
 hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const* xs, int x_dtype,

@@ -390,7 +390,8 @@ static GemmPlan plan_gemm(int M, int N, int K, int batch, int num_cus) {
             const int64_t slots = (int64_t)num_cus * c.per_cu;
             const int64_t rounds = (tiles + slots - 1) / slots;
             const double block_flops = 2.0 * c.bm * c.bn * (double)ss * c.bk;
-            double t = rounds * block_flops / (c.eff * 1e12 / (double)slots);
+            const double eff = c.eff > 0 ? c.eff : 100.0;              // unmeasured tuning tiles
+            double t = rounds * block_flops / (eff * 1e12 / (double)slots);
             if (splits > 1) t += (double)M * N * batch * 4.0 * (2.0 * splits + 1.0) / 4e12 + 3e-6;
             if (t < best_t) { best_t = t; best = GemmPlan{&c, splits, ss}; }
         }

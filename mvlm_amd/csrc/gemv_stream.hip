@@ -1,5 +1,7 @@
-// Decode GEMV (M = 1) for every packed weight format, one or several
-// independent problems per launch:  y_p[n] = sum_k x_p[k] * w_p(n, k).
+// Decode GEMV for every packed weight format, one or several independent
+// problems per launch:  y_p[m][n] = sum_k x_p[m][k] * w_p(n, k), M = 1 (and,
+// for quantized weights, M <= 4: batched decode, every weight chunk converted
+// once and multiplied with the M rows of x).
 //
 // Replaces gemv (src/kernels/gemm.cl:215-270) and adds the dequantizing
 // Q8_0 / Q4_0 GEMV the reference plans (README.md:57).  A decode GEMV is one
@@ -38,6 +40,7 @@ template <typename WT>
 struct DenseFmt {
     static constexpr int WPL = 16 / (int)sizeof(WT);   // weights per lane per chunk
     static constexpr bool QUANT = false;
+    static constexpr int MIN_WAVES_BATCH = 4;          // (dense weights take M = 1 only)
     static constexpr int MIN_WAVES = 8;                // per SIMD: 4 blocks of 8 waves per CU
 };
 
@@ -45,12 +48,14 @@ struct Q8Fmt {
     static constexpr int WPL = 16;
     static constexpr bool QUANT = true;
     static constexpr int MIN_WAVES = 8;
+    static constexpr int MIN_WAVES_BATCH = 4;          // 4 rows of x
 };
 
 struct Q4Fmt {
     static constexpr int WPL = 32;
     static constexpr bool QUANT = true;
     static constexpr int MIN_WAVES = 4;                // 32 x values per lane need more registers
+    static constexpr int MIN_WAVES_BATCH = 2;          // and 4 rows of x 4x as many
 };
 
 // x values of one chunk as raw bits: E elements of XT in XD dwords.
@@ -149,12 +154,13 @@ __device__ __forceinline__ void stage_to_lds(uint8_t* dst, const uint8_t* __rest
 // first vector instead (always in bounds) and discard the result, which keeps
 // every load unconditional and lets them all issue before the first wait.
 struct StreamProblem {
-    const void* x;
+    const void* x;                 // [M][K]
     const uint8_t* codes;
     const uint16_t* scales;
-    void* y;
+    void* y;                       // [M][N]
     int64_t ld_bytes;
     int N, K, y_dtype;
+    int M;                         // rows of x (1 for MX = 1; 1..4 for MX = 4)
     int shape;                     // index into kShapes
     int rows_per_block;            // block j owns rows [j*rows_per_block, (j+1)*rows_per_block) below N
     int block_begin;               // first block of this problem in the grid
@@ -183,12 +189,14 @@ constexpr int kNumShapes = 5;
 static_assert(sizeof(kShapes) / sizeof(kShapes[0]) == kNumShapes, "one kernel case per shape");
 
 // The rows [row0, row0 + R) of one wave (those below the block's end rb1),
-// its chunks wsub*CW ... of each.
-// x and the scales are already being staged into LDS (staging loads were
-// issued before these and complete first).
-template <class F, typename XT, int R, int CW, int SPLIT>
-__device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int rb1, int64_t s_base, int x_region,
-                                            const uint8_t* lds, float (*part)[4], int wave, int lane) {
+// its chunks wsub*CW ... of each, against MX rows of x (vector m staged at
+// LDS byte m * x_stride; rows of x at or past M repeat row M-1 and are not
+// stored).  x and the scales are already being staged into LDS (staging loads
+// were issued before these and complete first).
+template <class F, typename XT, int MX, int R, int CW, int SPLIT>
+__device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int rb1, int64_t s_base, int x_stride,
+                                            int x_region, const uint8_t* lds, float (*part)[16], int wave,
+                                            int lane) {
     constexpr int WPL = F::WPL;
     constexpr int XB = WPL * (int)sizeof(XT);        // x bytes per lane per chunk
     constexpr int SL = XB >= 16 ? XB / 16 : 1;       // 16-byte LDS slots per lane per chunk
@@ -225,58 +233,99 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
     wait_vmcnt<R * CW>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    float acc[R];
+    float acc[R][MX];
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MX; ++m) acc[r][m] = 0.0f;
 #pragma unroll
     for (int i = 0; i < CW; ++i) {
-        XRaw<XT, WPL> xr;
-        const int xbyte = kk[i] * (int)sizeof(XT);
-        if constexpr (XB >= 16) {
+        if constexpr (MX == 1) {   // one row of x: the x slice is read once per chunk
+            XRaw<XT, WPL> xr;
+            const int xbyte = kk[i] * (int)sizeof(XT);
+            if constexpr (XB >= 16) {
 #pragma unroll
-            for (int v = 0; v < SL; ++v) {
-                const u32x4 u = reinterpret_cast<const u32x4*>(lds)[x_slot<SL>((xbyte >> 4) + v)];
-                xr.d[4 * v + 0] = u[0]; xr.d[4 * v + 1] = u[1];
-                xr.d[4 * v + 2] = u[2]; xr.d[4 * v + 3] = u[3];
+                for (int v = 0; v < SL; ++v) {
+                    const u32x4 u = reinterpret_cast<const u32x4*>(lds)[x_slot<SL>((xbyte >> 4) + v)];
+                    xr.d[4 * v + 0] = u[0]; xr.d[4 * v + 1] = u[1];
+                    xr.d[4 * v + 2] = u[2]; xr.d[4 * v + 3] = u[3];
+                }
+            } else {   // XB == 8
+                const u32x2 u = *reinterpret_cast<const u32x2*>(lds + xbyte);
+                xr.d[0] = u[0]; xr.d[1] = u[1];
             }
-        } else {   // XB == 8
-            const u32x2 u = *reinterpret_cast<const u32x2*>(lds + xbyte);
-            xr.d[0] = u[0]; xr.d[1] = u[1];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                uint16_t dh = 0;
+                if constexpr (F::QUANT)
+                    dh = *reinterpret_cast<const uint16_t*>(lds + x_region + srow[r] + (kk[i] >> 5) * 2);
+                const float v = chunk_dot(F{}, q[r][i], dh, xr, acc[r][0]);
+                acc[r][0] = valid[i] ? v : acc[r][0];
+            }
+            continue;
         }
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            uint16_t dh = 0;
-            if constexpr (F::QUANT) dh = *reinterpret_cast<const uint16_t*>(lds + x_region + srow[r] + (kk[i] >> 5) * 2);
-            const float v = chunk_dot(F{}, q[r][i], dh, xr, acc[r]);
-            acc[r] = valid[i] ? v : acc[r];
+        for (int m = 0; m < MX; ++m) {
+            XRaw<XT, WPL> xr;
+            const uint8_t* xl = lds + m * x_stride;
+            const int xbyte = kk[i] * (int)sizeof(XT);
+            if constexpr (XB >= 16) {
+#pragma unroll
+                for (int v = 0; v < SL; ++v) {
+                    const u32x4 u = reinterpret_cast<const u32x4*>(xl)[x_slot<SL>((xbyte >> 4) + v)];
+                    xr.d[4 * v + 0] = u[0]; xr.d[4 * v + 1] = u[1];
+                    xr.d[4 * v + 2] = u[2]; xr.d[4 * v + 3] = u[3];
+                }
+            } else {   // XB == 8
+                const u32x2 u = *reinterpret_cast<const u32x2*>(xl + xbyte);
+                xr.d[0] = u[0]; xr.d[1] = u[1];
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                uint16_t dh = 0;
+                if constexpr (F::QUANT)
+                    dh = *reinterpret_cast<const uint16_t*>(lds + x_region + srow[r] + (kk[i] >> 5) * 2);
+                const float v = chunk_dot(F{}, q[r][i], dh, xr, acc[r][m]);
+                acc[r][m] = valid[i] ? v : acc[r][m];
+            }
         }
     }
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MX; ++m) acc[r][m] = wave_sum(acc[r][m]);
 
+    // y[m][row] (and the epilogue's mul / residual [m][row], bias [row])
+    auto store_row = [&](int row, int m, float v) {
+        const int64_t idx = (int64_t)m * P.N + row;
+        store_out(P.y, idx, P.ep_on ? apply_epilogue(P.ep, v, idx, row) : v, P.y_dtype);
+    };
     if constexpr (SPLIT == 1) {
         if (lane == 0 && active) {
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                if (row0 + r < rb1)
-                    store_out(P.y, row0 + r, P.ep_on ? apply_epilogue(P.ep, acc[r], row0 + r, row0 + r) : acc[r],
-                              P.y_dtype);
+#pragma unroll
+                for (int m = 0; m < MX; ++m)
+                    if (row0 + r < rb1 && m < P.M) store_row(row0 + r, m, acc[r][m]);
         }
     } else {
         if (lane == 0) {
 #pragma unroll
-            for (int r = 0; r < R; ++r) part[wave][r] = acc[r];
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int m = 0; m < MX; ++m) part[wave][r * MX + m] = acc[r][m];
         }
         __syncthreads();
         if (wsub == 0 && lane == 0 && active) {
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                float v = part[wave][r];
+            for (int r = 0; r < R; ++r)
 #pragma unroll
-                for (int s = 1; s < SPLIT; ++s) v += part[wave + s][r];
-                if (row0 + r < rb1)
-                    store_out(P.y, row0 + r, P.ep_on ? apply_epilogue(P.ep, v, row0 + r, row0 + r) : v, P.y_dtype);
-            }
+                for (int m = 0; m < MX; ++m) {
+                    float v = part[wave][r * MX + m];
+#pragma unroll
+                    for (int s = 1; s < SPLIT; ++s) v += part[wave + s][r * MX + m];
+                    if (row0 + r < rb1 && m < P.M) store_row(row0 + r, m, v);
+                }
         }
     }
 }
@@ -289,12 +338,13 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
 // registers.  Issue order: x and scale staging, then every code load, then
 // the wait for the staging alone (vmcnt counts in issue order), the block
 // barrier, the LDS reads, and the wait for the codes.
-template <class F, typename XT>
-__global__ __launch_bounds__(64 * NWAVE, F::MIN_WAVES) void gemv_stream_kernel(const StreamGroup g) {
+template <class F, typename XT, int MX>
+__global__ __launch_bounds__(64 * NWAVE, MX == 1 ? F::MIN_WAVES : F::MIN_WAVES_BATCH) void gemv_stream_kernel(
+    const StreamGroup g) {
     constexpr int XB = F::WPL * (int)sizeof(XT);
     constexpr int SL = XB >= 16 ? XB / 16 : 1;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    __shared__ float part[NWAVE][4];
+    __shared__ float part[NWAVE][16];
 
     int pi = 0;
 #pragma unroll
@@ -308,11 +358,16 @@ __global__ __launch_bounds__(64 * NWAVE, F::MIN_WAVES) void gemv_stream_kernel(c
     const int rb0 = ((int)blockIdx.x - P.block_begin) * P.rows_per_block;
     const int rb1 = min(rb0 + P.rows_per_block, N);
 
-    // stage x (and the block's scales) in LDS
+    // stage the MX rows of x (and the block's scales) in LDS
     // (x_bytes is a multiple of XB, so of 16 when XB >= 16)
     const int x_bytes = K * (int)sizeof(XT);
-    const int x_region = (x_bytes + 1023) & ~1023;
-    stage_to_lds<(XB >= 16 ? 16 : 4), SL, NWAVE>(lds, (const uint8_t*)P.x, x_bytes, wave, lane);
+    const int x_stride = (x_bytes + 1023) & ~1023;
+    const int x_region = MX * x_stride;
+#pragma unroll
+    for (int m = 0; m < MX; ++m)
+        stage_to_lds<(XB >= 16 ? 16 : 4), SL, NWAVE>(lds + m * x_stride,
+                                                    (const uint8_t*)P.x + (m == 0 ? 0 : (int64_t)min(m, P.M - 1) * x_bytes),
+                                                    x_bytes, wave, lane);
     int64_t s_base = 0;                               // global byte offset of the first staged scale byte
     if constexpr (F::QUANT) {
         const int64_t s_begin = (int64_t)rb0 * (nb * 2);
@@ -326,8 +381,8 @@ __global__ __launch_bounds__(64 * NWAVE, F::MIN_WAVES) void gemv_stream_kernel(c
     switch (P.shape) {   // uniform over the block
 #define MVLM_SHAPE_CASE(i)                                                                               \
     case i:                                                                                              \
-        stream_rows<F, XT, kShapes[i].R, kShapes[i].CW, kShapes[i].SPLIT>(P, rb0, rb1, s_base, x_region, \
-                                                                           lds, part, wave, lane);       \
+        stream_rows<F, XT, MX, kShapes[i].R, kShapes[i].CW, kShapes[i].SPLIT>(P, rb0, rb1, s_base, x_stride, \
+                                                                               x_region, lds, part, wave, lane); \
         break;
         MVLM_SHAPE_CASE(0) MVLM_SHAPE_CASE(1) MVLM_SHAPE_CASE(2) MVLM_SHAPE_CASE(3) MVLM_SHAPE_CASE(4)
 #undef MVLM_SHAPE_CASE
@@ -354,9 +409,9 @@ static int rows_per_block(int shape) { return kShapes[shape].R * (NWAVE / kShape
 // slack of their start, each rounded to the 1 KiB pieces the staging writes.
 // Scale reads reach up to 15 bytes past the scale array, which the weight
 // allocation pads.
-static size_t stream_lds_bytes(const mvlm_weight* w, int x_dtype, int shape) {
+static size_t stream_lds_bytes(const mvlm_weight* w, int x_dtype, int shape, int mx = 1) {
     const size_t x_bytes = (size_t)w->K * dtype_size(x_dtype);
-    size_t bytes = (x_bytes + 1023) & ~(size_t)1023;
+    size_t bytes = (size_t)mx * ((x_bytes + 1023) & ~(size_t)1023);
     if (is_quant(w->dtype))
         bytes += ((size_t)rows_per_block(shape) * (size_t)(w->K / 32) * 2 + 30 + 1023) & ~(size_t)1023;
     return bytes;
@@ -364,9 +419,11 @@ static size_t stream_lds_bytes(const mvlm_weight* w, int x_dtype, int shape) {
 
 constexpr size_t STREAM_LDS_MAX = 152 * 1024;
 
-bool stream_supported(const mvlm_weight* w) {
+bool stream_supported(const mvlm_weight* w, int M) {
     const int shape = stream_shape(w);
-    return shape >= 0 && w->K % weight_wpl(w->dtype) == 0 && stream_lds_bytes(w, MVLM_F32, shape) <= STREAM_LDS_MAX;
+    if (M > 1 && (M > 4 || !is_quant(w->dtype))) return false;
+    return shape >= 0 && w->K % weight_wpl(w->dtype) == 0 &&
+           stream_lds_bytes(w, MVLM_F32, shape, M > 1 ? 4 : 1) <= STREAM_LDS_MAX;
 }
 
 int stream_max_group() { return MAX_GROUP; }
@@ -388,9 +445,9 @@ static unsigned partition(StreamGroup& g) {
     return begin;
 }
 
-template <class F, typename XT>
+template <class F, typename XT, int MX = 1>
 static hipError_t launch_group(hipStream_t s, StreamGroup& g, size_t lds) {
-    auto kernel = gemv_stream_kernel<F, XT>;
+    auto kernel = gemv_stream_kernel<F, XT, MX>;
     static bool attr_set = false;
     if (!attr_set) {
         const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -433,6 +490,7 @@ hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const*
         p.N = w->N;
         p.K = w->K;
         p.y_dtype = y_dtypes[i];
+        p.M = 1;
         p.shape = stream_shape(w);
         if (eps && eps[i].any()) {
             p.ep = eps[i];
@@ -457,6 +515,34 @@ hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const*
 hipError_t launch_gemv_stream(hipStream_t s, const void* x, int x_dtype, const mvlm_weight* W, void* y,
                               int y_dtype, int num_cus, const Epilogue* ep) {
     return launch_gemv_stream_group(s, 1, &x, x_dtype, &W, &y, &y_dtype, num_cus, ep);
+}
+
+// Quantized weight, fp32 x [M][K] and y [M][N], 2 <= M <= 4.
+hipError_t launch_gemv_stream_batch(hipStream_t s, const float* x, const mvlm_weight* W, float* y, int M,
+                                    int num_cus, const Epilogue* ep) {
+    (void)num_cus;
+    if (M < 2 || M > 4 || !stream_supported(W, M)) return hipErrorInvalidValue;
+    StreamGroup g{};
+    g.count = 1;
+    StreamProblem& p = g.p[0];
+    p.x = x;
+    p.codes = (const uint8_t*)W->data;
+    p.scales = (const uint16_t*)W->scales;
+    p.y = y;
+    p.ld_bytes = weight_row_bytes(W);
+    p.N = W->N;
+    p.K = W->K;
+    p.y_dtype = MVLM_F32;
+    p.M = M;
+    p.shape = stream_shape(W);
+    if (ep && ep->any()) {
+        p.ep = *ep;
+        p.ep_on = 1;
+    }
+    const size_t lds = stream_lds_bytes(W, MVLM_F32, p.shape, 4);
+    if (W->dtype == MVLM_Q8_0) return launch_group<Q8Fmt, float, 4>(s, g, lds);
+    if (W->dtype == MVLM_Q4_0) return launch_group<Q4Fmt, float, 4>(s, g, lds);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace mvlm

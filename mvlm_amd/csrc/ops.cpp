@@ -284,6 +284,8 @@ hipError_t enqueue_op(hipStream_t s, const Op& op) {
         case OP_GEMV_QUANT:
             if (op.M == 1 && stream_supported(op.w))
                 return launch_gemv_stream(s, op.a, MVLM_F32, op.w, op.c, MVLM_F32, op.num_cus, &op.ep);
+            if (op.M <= 4 && stream_supported(op.w, op.M))
+                return launch_gemv_stream_batch(s, (const float*)op.a, op.w, (float*)op.c, op.M, op.num_cus, &op.ep);
             return launch_gemm_skinny(s, (const float*)op.a, op.w, (float*)op.c, op.M, op.N, op.K, op.num_cus,
                                       &op.ep);
         case OP_ARGMAX:
