@@ -195,7 +195,7 @@ static_assert(sizeof(kShapes) / sizeof(kShapes[0]) == kNumShapes, "one kernel ca
 // were issued before these and complete first).
 template <class F, typename XT, int MX, int R, int CW, int SPLIT>
 __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int rb1, int64_t s_base, int x_stride,
-                                            int x_region, const uint8_t* lds, float (*part)[16], int wave,
+                                            int x_region, const uint8_t* lds, float (*part)[4 * MX], int wave,
                                             int lane) {
     constexpr int WPL = F::WPL;
     constexpr int XB = WPL * (int)sizeof(XT);        // x bytes per lane per chunk
@@ -297,8 +297,12 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
 
     // y[m][row] (and the epilogue's mul / residual [m][row], bias [row])
     auto store_row = [&](int row, int m, float v) {
-        const int64_t idx = (int64_t)m * P.N + row;
-        store_out(P.y, idx, P.ep_on ? apply_epilogue(P.ep, v, idx, row) : v, P.y_dtype);
+        if constexpr (MX == 1) {
+            store_out(P.y, row, P.ep_on ? apply_epilogue(P.ep, v, row, row) : v, P.y_dtype);
+        } else {
+            const int64_t idx = (int64_t)m * P.N + row;
+            store_out(P.y, idx, P.ep_on ? apply_epilogue(P.ep, v, idx, row) : v, P.y_dtype);
+        }
     };
     if constexpr (SPLIT == 1) {
         if (lane == 0 && active) {
@@ -306,7 +310,7 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
             for (int r = 0; r < R; ++r)
 #pragma unroll
                 for (int m = 0; m < MX; ++m)
-                    if (row0 + r < rb1 && m < P.M) store_row(row0 + r, m, acc[r][m]);
+                    if (row0 + r < rb1 && (MX == 1 || m < P.M)) store_row(row0 + r, m, acc[r][m]);
         }
     } else {
         if (lane == 0) {
@@ -324,7 +328,7 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
                     float v = part[wave][r * MX + m];
 #pragma unroll
                     for (int s = 1; s < SPLIT; ++s) v += part[wave + s][r * MX + m];
-                    if (row0 + r < rb1 && m < P.M) store_row(row0 + r, m, v);
+                    if (row0 + r < rb1 && (MX == 1 || m < P.M)) store_row(row0 + r, m, v);
                 }
         }
     }
@@ -344,7 +348,7 @@ __global__ __launch_bounds__(64 * NWAVE, MX == 1 ? F::MIN_WAVES : F::MIN_WAVES_B
     constexpr int XB = F::WPL * (int)sizeof(XT);
     constexpr int SL = XB >= 16 ? XB / 16 : 1;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    __shared__ float part[NWAVE][16];
+    __shared__ float part[NWAVE][4 * MX];
 
     int pi = 0;
 #pragma unroll
