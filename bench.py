@@ -242,6 +242,24 @@ def token_pick(dev, m, steps, warmup):
     return res
 
 
+GEMM_SHAPES = (("phi15_prefill_qkv", 768, 6144, 2048), ("phi15_prefill_fc1", 768, 8192, 2048),
+               ("phi15_prefill_fc2", 768, 2048, 8192), ("siglip_qkv", 729, 3456, 1152),
+               ("siglip_out", 729, 1152, 1152), ("siglip_fc1", 729, 4304, 1152),
+               ("siglip_fc2", 729, 1152, 4304))
+
+
+def gemm_extras(dev, m, steps, warmup, extra):
+    """The M = 729 / 768 fp16 GEMMs (Phi-1.5 prefill, SigLIP) and the batched QK^T."""
+    for name, M, N, K in GEMM_SHAPES:
+        r = gemm_shape(dev, m, name, M, N, K, steps, warmup)
+        extra[name] = r
+        log(f"[bench]   {name} {M}x{N}x{K}: {r['us']:.1f} us {r['tflops']:.0f} TFLOP/s "
+            f"({100 * r['frac']:.1f}% of 2.5 PF)")
+    r = qk_batched(dev, m, steps, warmup)
+    extra[r["workload"]] = r
+    log(f"[bench]   {r['workload']}: {r['us']:.1f} us {r['tflops']:.0f} TFLOP/s {r['gbs']:.0f} GB/s")
+
+
 def f4_extras(dev, m, steps, warmup, extra):
     for name, sq, skv, H, D, causal in ATTENTION_SHAPES:
         r = attention_shape(dev, m, name, sq, skv, H, D, causal, steps, warmup)
@@ -374,6 +392,8 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true", help="workload for rocprofv3 --pmc traffic runs")
     ap.add_argument("--attention-only", action="store_true",
                     help="only the attention and token-pick workloads (one JSON line of them)")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="only the prefill / vision GEMM shapes and the batched QK^T (one JSON line of them)")
     ap.add_argument("--pmc-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn the two counter runs into " + os.path.relpath(TRAFFIC_FILE, ROOT))
     args = ap.parse_args()
@@ -393,9 +413,12 @@ def main():
     info = dev.info()
     log(f"[bench] {info.device_name.decode()} {info.arch_name.decode()} CUs={info.compute_units} "
         f"clock={info.max_clock_mhz} MHz HBM={info.global_mem_size / 2**30:.0f} GiB")
-    if args.attention_only:
+    if args.attention_only or args.gemm_only:
         extra = {}
-        f4_extras(dev, m, 20, 5, extra)
+        if args.gemm_only:
+            gemm_extras(dev, m, 20, 5, extra)
+        if args.attention_only:
+            f4_extras(dev, m, 20, 5, extra)
         dev.close()
         print(json.dumps({"workloads": extra}), flush=True)
         return
@@ -416,17 +439,7 @@ def main():
         r = fp32_gemv(dev, m, max(10, args.steps // 2), 3)
         extra[r["workload"]] = r
         log(f"[bench]   {r['workload']}: {r['us']:.1f} us {r['gbs']:.0f} GB/s ({100 * r['frac']:.1f}%)")
-        for name, M, N, K in (("phi15_prefill_qkv", 768, 6144, 2048), ("phi15_prefill_fc1", 768, 8192, 2048),
-                              ("phi15_prefill_fc2", 768, 2048, 8192), ("siglip_qkv", 729, 3456, 1152),
-                              ("siglip_out", 729, 1152, 1152), ("siglip_fc1", 729, 4304, 1152),
-                              ("siglip_fc2", 729, 1152, 4304)):
-            r = gemm_shape(dev, m, name, M, N, K, 20, 5)
-            extra[name] = r
-            log(f"[bench]   {name} {M}x{N}x{K}: {r['us']:.1f} us {r['tflops']:.0f} TFLOP/s "
-                f"({100 * r['frac']:.1f}% of 2.5 PF)")
-        r = qk_batched(dev, m, 20, 5)
-        extra[r["workload"]] = r
-        log(f"[bench]   {r['workload']}: {r['us']:.1f} us {r['tflops']:.0f} TFLOP/s {r['gbs']:.0f} GB/s")
+        gemm_extras(dev, m, 20, 5, extra)
         f4_extras(dev, m, 20, 5, extra)
 
     cpu = None

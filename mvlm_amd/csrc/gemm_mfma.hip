@@ -376,6 +376,13 @@ static GemmPlan plan_gemm(int M, int N, int K, int batch, int num_cus) {
     }
     const char* fs = std::getenv("MVLM_GEMM_SPLITS");
     const int forced_splits = fs ? std::atoi(fs) : 0;
+    // K <= 128 (e.g. attention scores, head_dim 72): a block's time is its load
+    // latency and its C store, not its MFMAs, which the model above does not
+    // see; 128x128 tiles with 32-wide stages (less K padding, two blocks per
+    // CU) measured fastest there (16 x 729x729x72: 19.9 us vs 25.2 us).
+    if (!forced && K <= 128 && forced_splits <= 1)
+        for (const TileCfg& c : kTiles)
+            if (c.bm == 128 && c.bn == 128 && c.bk == 32 && c.per_cu == 2) forced = &c;
     const int n_cand = forced ? 1 : kAutoTiles;
     for (int i = 0; i < n_cand; ++i) {
         const TileCfg& c = forced ? *forced : kTiles[i];
