@@ -18,18 +18,21 @@
 //    accumulator column is query l%32 and register r is key
 //    8(r/4) + 4(l/32) + r%4, so a query's softmax statistics are per lane
 //    (plus one exchange with lane l^32);
-//  * O^T = V^T P^T: A = V^T (the V tile stored transposed in LDS), B = the
-//    lane's own probabilities packed to fp16: register r's key order above is
-//    taken as the k order of the product, so A reads V^T columns
-//    {4h..4h+3, 8+4h..8+4h+3} (+16 per k-step) to match, and no data moves
-//    between lanes;
+//  * O^T = V^T P^T: A = V^T, B = the lane's own probabilities packed to
+//    fp16: register r's key order above is taken as the k order of the
+//    product, so A holds keys {4h..4h+3, 8+4h..8+4h+3} (+16 per k-step) to
+//    match, and no data moves between lanes.  V is stored row-major in LDS
+//    (like K) and its transposed fragments come from ds_read_b64_tr_b16
+//    (within 16 lanes, lane j receives element j%4 of the 4-element rows read
+//    by lanes 4k + j/4, k = 0..3): lane 4k + q reads 4 dims at 4q of key k, so
+//    lane j gets dim j of 4 consecutive keys;
 //  * the output accumulator O^T also has query l%32 per lane, so the online
 //    rescaling is one multiply per register;
 //  * every wave stages its own tiles (no block barrier in the key loop) and
 //    loads tile j+1 into registers while it computes tile j.
 // head_dim is padded to 16 KS (S^T k-steps) and 32 DT (O^T row tiles); the K
-// tile's padding columns are zeroed once, V^T padding rows only feed output
-// rows that are never stored.  Keys past the end are read from the last row
+// tile's padding columns are zeroed once, V's columns past head_dim (never
+// written) only feed output rows that are never stored.  Keys past the end are read from the last row
 // (finite data) and get score -inf.  Causal masking hides key k from query q
 // when k > q + (seq_kv - seq_q) (queries aligned to the end of the keys;
 // seq_q == seq_kv gives attention.cl's k > q) and skips the key tiles past
@@ -72,8 +75,11 @@ __device__ __forceinline__ float* attn_ws_ml(const AttnArgs& a, int64_t r) {
 template <int KS, int DT>
 struct AttnLayout {
     static constexpr int KROW = 16 * KS + 8;                  // K tile row pitch (halfs): odd multiple of 16 B
-    static constexpr int VROW = 36;                           // V^T row pitch (halfs): conflict-free b64 reads
-    static constexpr int STAGE = 32 * KROW * 2 + 32 * DT * VROW * 2;
+    // V tile row pitch (halfs): >= 32 DT (the transposed reads reach dim 32 DT - 1)
+    // and 32 mod 64, so the 4 key rows a 32-lane half of a transposed read
+    // touches start 16 banks apart (64 contiguous bytes each: all 64 banks)
+    static constexpr int VP = DT == 1 ? 32 : DT <= 3 ? 96 : 160;
+    static constexpr int STAGE = 32 * KROW * 2 + 32 * VP * 2;
     static constexpr int OPITCH = 32 * DT + 4;                // merge area row pitch (floats)
     static constexpr int MERGE = 32 * OPITCH * 4 + 2 * 32 * 4;
     static constexpr int REGION = ((STAGE > MERGE ? STAGE : MERGE) + 15) / 16 * 16;   // bytes per wave
@@ -88,6 +94,8 @@ __device__ __forceinline__ f32x16 mfma_f16(u32x4 a, u32x4 b, f32x16 c) {
 }
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 // two fp32 values to packed fp16, round to nearest even (one v_cvt_pk_f16_f32)
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
@@ -110,7 +118,7 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(const AttnArgs a) {
 
     uint8_t* region = lds + wave * L::REGION;
     uint16_t* ks = (uint16_t*)region;                     // [32 keys][KROW]
-    uint16_t* vt = (uint16_t*)(region + 32 * L::KROW * 2);   // [32 DT dims][VROW]
+    uint16_t* vt = (uint16_t*)(region + 32 * L::KROW * 2);   // [32 keys][VP]
 
     // zero the K tile's padding columns D .. 16 KS once (contracted with Q's
     // zeros): D is a multiple of 8, so whole 16-byte chunks, one row per lane
@@ -176,15 +184,7 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(const AttnArgs a) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) *reinterpret_cast<u32x4*>(ks + (key0 + u) * L::KROW + d) = tk[i][u];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    // dim d + j of keys key0 .. key0+3
-                    // v_perm_b32 picks bytes of {src0 (4..7), src1 (0..3)}: the low
-                    // halves (j even, selector 0x05040100) or the high halves (0x07060302)
-                    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-                    const uint32_t k01 = __builtin_amdgcn_perm(tv[i][1][j >> 1], tv[i][0][j >> 1], sel);
-                    const uint32_t k23 = __builtin_amdgcn_perm(tv[i][3][j >> 1], tv[i][2][j >> 1], sel);
-                    *reinterpret_cast<u32x2*>(vt + (d + j) * L::VROW + key0) = u32x2{k01, k23};
-                }
+                for (int u = 0; u < 4; ++u) *reinterpret_cast<u32x4*>(vt + (key0 + u) * L::VP + d) = tv[i][u];
             }
         }
     };
@@ -262,11 +262,16 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(const AttnArgs a) {
             u32x4 pb;
 #pragma unroll
             for (int j = 0; j < 4; ++j) pb[j] = pack_f16x2(p[8 * kk + 2 * j], p[8 * kk + 2 * j + 1]);
+            // lane l: dim 32t + l%32 of keys 16kk + 4h + 0..3 (lo) and +8 (hi):
+            // within its 16-lane group it reads key (l&15)>>2, dims 4(l&3)..+3
+            // of the group's 16 (l>>4 selects the half of the 32-dim tile)
+            const uint16_t* vgrp = vt + (16 * kk + 4 * h + ((lane & 15) >> 2)) * L::VP + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 #pragma unroll
             for (int t = 0; t < DT; ++t) {
-                const uint16_t* vrow = vt + (32 * t + l32) * L::VROW + 16 * kk + 4 * h;
-                const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
-                const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
+                lds_i16x4* p0 = (lds_i16x4*)(uintptr_t)lds_offset(vgrp + 32 * t);
+                lds_i16x4* p1 = (lds_i16x4*)(uintptr_t)lds_offset(vgrp + 32 * t + 8 * L::VP);
+                const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(p0));
+                const u32x2 hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(p1));
                 oacc[t] = mfma_f16(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb, oacc[t]);
             }
         }
