@@ -197,6 +197,7 @@ ATTENTION_SHAPES = [
     ("siglip_attention_16x729x72", 729, 729, 16, 72, False),
     ("phi15_prefill_attention_768_causal", 768, 768, 32, 64, True),
     ("phi15_decode_attention_cache2048", 1, 2048, 32, 64, False),
+    ("phi15_decode_attention_cache512", 1, 512, 32, 64, False),
 ]
 
 

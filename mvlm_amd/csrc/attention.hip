@@ -32,8 +32,8 @@
 //    loads tile j+1 into registers while it computes tile j.
 // head_dim is padded to 16 KS (S^T k-steps) and 32 DT (O^T row tiles); the K
 // tile's padding columns are zeroed once, V's columns past head_dim (never
-// written) only feed output rows that are never stored.  Keys past the end are read from the last row
-// (finite data) and get score -inf.  Causal masking hides key k from query q
+// written) only feed output rows that are never stored.  Keys past the end
+// read as zeros (buffer bounds check) and get score -inf.  Causal masking hides key k from query q
 // when k > q + (seq_kv - seq_q) (queries aligned to the end of the keys;
 // seq_q == seq_kv gives attention.cl's k > q) and skips the key tiles past
 // the block's last query.
@@ -433,12 +433,21 @@ static hipError_t launch_variant(hipStream_t s, const AttnArgs& a) {
 }
 
 // Splits over keys: none when the (32-query tile, head) blocks alone cover the
-// CUs; otherwise enough for about two blocks per CU, keeping at least two key
-// tiles per split.
+// CUs or the keys are at most 48 tiles (1536 keys); otherwise enough for about
+// two blocks per CU, keeping at least two key tiles per split.  The split path
+// pays a second launch (~3-4 us): one 32-head decode block per head with 16
+// waves measured 5.0 us against 9.3 us split at 512 keys, and 9.9 us against
+// 10.6-11.1 us split at 2048.
+// MVLM_ATTN_SPLITS=<n> forces the split count (tuning runs; read where the
+// workspace is sized and at every launch, so set it before creating the op).
 static int pick_splits(int seq_q, int seq_kv, int heads, int num_cus) {
     const int64_t blocks = (int64_t)(seq_q + 31) / 32 * heads;
     const int tiles = (seq_kv + 31) / 32;
-    if (blocks >= num_cus || tiles < 4) return 1;
+    if (const char* force = std::getenv("MVLM_ATTN_SPLITS")) {
+        const int f = std::atoi(force);
+        if (f >= 1 && f <= 32 && f <= tiles) return f;
+    }
+    if (blocks >= num_cus || tiles <= 48) return 1;
     const int64_t want = (2 * (int64_t)num_cus + blocks - 1) / blocks;
     return (int)std::max<int64_t>(1, std::min<int64_t>({want, tiles / 2, 32}));
 }

@@ -94,13 +94,22 @@ def test_attention_long_cache_decode(dev, orc):
     run(dev, orc, 4, 2048, 32, 64, True, F32, seed=10)
 
 
-@pytest.mark.parametrize("waves", ["1", "2", "16"])
-def test_attention_forced_waves_with_key_splits(dev, orc, monkeypatch, waves):
-    """few (query tile, head) blocks: the keys are split over workgroups and
-    merged by a second kernel; every waves-per-block variant must agree"""
+@pytest.mark.parametrize("waves,splits", [("1", "5"), ("2", "5"), ("16", "5"), ("4", "2"), ("2", "1")])
+def test_attention_forced_waves_with_key_splits(dev, orc, monkeypatch, waves, splits):
+    """few (query tile, head) blocks: the keys split over workgroups (forced
+    here; the automatic choice keeps short caches in one block) and merged by
+    a second kernel; every waves-per-block and split variant must agree"""
     monkeypatch.setenv("MVLM_ATTN_WAVES", waves)
+    monkeypatch.setenv("MVLM_ATTN_SPLITS", splits)
     run(dev, orc, 1, 700, 8, 64, False, F32, seed=41)
     run(dev, orc, 40, 300, 4, 72, True, F16, seed=42)
+
+
+def test_attention_long_cache_single_block(dev, orc, monkeypatch):
+    """a 2048-entry cache without key splits: 16 waves per (head) block, 4 key
+    tiles each, merged in LDS"""
+    monkeypatch.setenv("MVLM_ATTN_SPLITS", "1")
+    run(dev, orc, 1, 2048, 32, 64, False, F16, seed=43)
 
 
 def test_prefill_and_decode_entry_points(dev, orc):
