@@ -85,13 +85,16 @@ def build_decode_plan(dev, m, qt, M, grouped=True):
     gelu = dev.fill_normal(dev.alloc(M * 8192 * 4), m.F32, M * 8192, SEED ^ 0x13, 1.0)   # MLP hidden
     x_of = {"qkv": ln, "fc1": ln, "dense": attn, "fc2": gelu, "lm_head": ln}
     ys = {name: dev.alloc(M * N * 4) for name, N, _ in PHI_LAYER + [PHI_LM_HEAD]}
-    grouped = grouped and M == 1
     plan = m.Plan(dev)
     if grouped:
         for layer in range(24):
             w = dict(zip(("qkv", "dense", "fc1", "fc2"), weights[4 * layer: 4 * layer + 4]))
-            plan.add_gemv_grouped([(x_of[n], m.F32, w[n], ys[n], m.F32) for n in ("qkv", "fc1")])
-            plan.add_gemv_grouped([(x_of[n], m.F32, w[n], ys[n], m.F32) for n in ("dense", "fc2")])
+            for pair in (("qkv", "fc1"), ("dense", "fc2")):
+                entries = [(x_of[n], m.F32, w[n], ys[n], m.F32) for n in pair]
+                if M == 1:
+                    plan.add_gemv_grouped(entries)
+                else:
+                    plan.add_gemm_quant_grouped(M, entries)
         plan.add_gemv(ln, m.F32, weights[-1], ys["lm_head"], m.F32, M)
     else:
         for W, (name, N, K) in zip(weights, PHI_STEP):
@@ -120,7 +123,7 @@ def decode_step(dev, m, qt, M, steps, warmup, graph=True, grouped=True):
     else:
         launch_names = [name for name, _, _ in PHI_STEP]
     res = {
-        "workload": f"phi15_decode_{qt}_m{M}" + ("" if grouped or M > 1 else "_ungrouped"), "M": M,
+        "workload": f"phi15_decode_{qt}_m{M}" + ("" if grouped else "_ungrouped"), "M": M,
         "gemvs": len(PHI_STEP), "launches": len(launch_names),
         "bytes_per_step": step_bytes, "ms_per_step": ms, "gbs": step_bytes / ms / 1e6,
         "kernel_ms_sum": kernel_ms, "kernel_gbs": step_bytes / kernel_ms / 1e6,

@@ -201,6 +201,11 @@ typedef struct mvlm_gemv_desc {
     int y_dtype;
 } mvlm_gemv_desc;
 int mvlm_gemv_grouped(mvlm_device* dev, int count, const mvlm_gemv_desc* descs, mvlm_event** ev);
+/* The same grouping for M rows of activations over Q8_0 / Q4_0 weights
+ * (batched decode; the reference has no batched path): each entry is
+ * Y[M,N] = X[M,K] * W^T with fp32 X and Y and the checks of mvlm_gemm_q8_0 /
+ * mvlm_gemm_q4_0, 1 <= M <= 16, one weight dtype for all entries. */
+int mvlm_gemm_quant_grouped(mvlm_device* dev, int M, int count, const mvlm_gemv_desc* descs, mvlm_event** ev);
 
 /* ---- dequantizing GEMV / skinny GEMM (planned in README.md:57, PLAN.md:65) */
 /* y[N] = x[K] * W^T, W packed Q8_0, x and y fp32. */
@@ -291,6 +296,7 @@ int mvlm_plan_size(const mvlm_plan* plan);
 int mvlm_plan_add_gemv(mvlm_plan* plan, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W,
                        mvlm_buffer* y, int y_dtype, int M);
 int mvlm_plan_add_gemv_grouped(mvlm_plan* plan, int count, const mvlm_gemv_desc* descs);
+int mvlm_plan_add_gemm_quant_grouped(mvlm_plan* plan, int M, int count, const mvlm_gemv_desc* descs);
 /* plan entries with a fused epilogue (mvlm_gemv_ex, M == 1; mvlm_gemm_packed_ex) */
 int mvlm_plan_add_gemv_ex(mvlm_plan* plan, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W,
                           mvlm_buffer* y, int y_dtype, const mvlm_epilogue* ep);

@@ -176,9 +176,16 @@ hipError_t launch_gemv_stream_batch(hipStream_t s, const float* x, const mvlm_we
                                     int num_cus, const Epilogue* ep = nullptr);
 hipError_t launch_gemv_stream(hipStream_t s, const void* x, int x_dtype, const mvlm_weight* W, void* y,
                               int y_dtype, int num_cus, const Epilogue* ep = nullptr);
+// One launch for up to 8 independent problems of one weight dtype and x dtype;
+// M > 1 (quantized weights, fp32 x and y, M <= 4) streams each weight once for
+// its M rows of x.
 hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const* xs, int x_dtype,
                                     const mvlm_weight* const* ws, void* const* ys, const int* y_dtypes, int num_cus,
-                                    const Epilogue* eps = nullptr);
+                                    const Epilogue* eps = nullptr, int M = 1);
+// Skinny GEMM over up to 8 independent problems (quantized weights of one
+// dtype, fp32 X [M][K] and Y [M][N] each, 1 <= M <= 16) in one launch.
+hipError_t launch_gemm_skinny_group(hipStream_t s, int M, int count, const float* const* Xs,
+                                    const mvlm_weight* const* ws, float* const* Ys, int num_cus);
 inline int64_t weight_row_bytes(const mvlm_weight* w) { return is_dense(w->dtype) ? w->ld * (int64_t)dtype_size(w->dtype) : w->ld; }
 // MFMA GEMM; a K split (chosen by the launcher's cost model) needs
 // gemm_workspace_bytes(...) bytes of workspace

@@ -41,6 +41,8 @@
 #include "common.h"
 #include "device_math.h"
 
+#include <algorithm>
+
 namespace mvlm {
 
 
@@ -115,12 +117,26 @@ static size_t skinny_lds_bytes(int K) {
     return scale_region + (size_t)NW * 2 * skinny_slot_bytes<Q4, R, NW>();
 }
 
+// One problem of a (possibly grouped) launch: Y[M][N] = X[M][K] w^T.
+struct SkinnyProblem {
+    const float* X;
+    const uint8_t* codes;
+    const uint16_t* scales;
+    float* Y;
+    int64_t ld;
+    int N, K;
+    int block_begin;               // first block of this problem in the grid
+    int ep_on;
+    Epilogue ep;
+};
+constexpr int SKINNY_MAX_GROUP = 8;
+struct SkinnyGroup {
+    SkinnyProblem p[SKINNY_MAX_GROUP];
+    int count, M;
+};
+
 template <bool Q4, int R, int NW>
-__global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(const float* __restrict__ X,
-                                                              const uint8_t* __restrict__ codes,
-                                                              const uint16_t* __restrict__ scales,
-                                                              float* __restrict__ Y, int M, int N, int K,
-                                                              int64_t ld, const Epilogue ep, int ep_on) {
+__global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(const SkinnyGroup g) {
     using L = SkinnyLayout<Q4>;
     constexpr int ROWS = 16 * R;
     constexpr int SLOT = skinny_slot_bytes<Q4, R, NW>();
@@ -128,9 +144,21 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(const float* __res
     static_assert(NDMA <= 63, "direct loads of one step must fit vmcnt");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
+    int pi = 0;                                       // blocks are dealt to the problems in order
+#pragma unroll
+    for (int i = 1; i < SKINNY_MAX_GROUP; ++i)
+        if (i < g.count && (int)blockIdx.x >= g.p[i].block_begin) pi = i;
+    const SkinnyProblem& P = g.p[pi];
+    const float* __restrict__ X = P.X;
+    const uint8_t* __restrict__ codes = P.codes;
+    const uint16_t* __restrict__ scales = P.scales;
+    float* __restrict__ Y = P.Y;
+    const int M = g.M, N = P.N, K = P.K;
+    const int64_t ld = P.ld;
+
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15, q = lane >> 4;
-    const int n0 = blockIdx.x * ROWS;
+    const int n0 = ((int)blockIdx.x - P.block_begin) * ROWS;
     const int nb = K >> 5;
     const int per = (nb + NW - 1) / NW;
     const int b0 = wave * per, b1 = min(b0 + per, nb);
@@ -277,7 +305,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(const float* __res
                 const int m = 4 * q + i;
                 if (m < M) {
                     const int64_t idx = (int64_t)m * N + n;
-                    Y[idx] = ep_on ? apply_epilogue(ep, sum[i], idx, n) : sum[i];
+                    Y[idx] = P.ep_on ? apply_epilogue(P.ep, sum[i], idx, n) : sum[i];
                 }
             }
         }
@@ -285,10 +313,15 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(const float* __res
 }
 
 template <bool Q4, int R, int NW>
-static hipError_t launch_skinny(hipStream_t s, const float* X, const mvlm_weight* W, float* Y, int M, int N, int K,
-                                const Epilogue& ep) {
+static hipError_t launch_skinny(hipStream_t s, SkinnyGroup& g) {
     auto kernel = gemm_skinny_kernel<Q4, R, NW>;
-    const size_t lds = skinny_lds_bytes<Q4, R, NW>(K);
+    size_t lds = 0;
+    unsigned blocks = 0;
+    for (int i = 0; i < g.count; ++i) {
+        lds = std::max(lds, skinny_lds_bytes<Q4, R, NW>(g.p[i].K));
+        g.p[i].block_begin = (int)blocks;
+        blocks += (unsigned)((g.p[i].N + 16 * R - 1) / (16 * R));
+    }
     static bool attr_set = false;
     if (!attr_set) {
         const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -297,31 +330,64 @@ static hipError_t launch_skinny(hipStream_t s, const float* X, const mvlm_weight
         attr_set = true;
     }
     if (lds > SKINNY_LDS_MAX) return hipErrorInvalidValue;
-    const unsigned blocks = (unsigned)((N + 16 * R - 1) / (16 * R));
-    launch_kernel(kernel, dim3(blocks), dim3(64 * NW), (uint32_t)lds, s, X, (const uint8_t*)W->data,
-                  (const uint16_t*)W->scales, Y, M, N, K, (int64_t)W->ld, ep, ep.any() ? 1 : 0);
+    launch_kernel(kernel, dim3(blocks), dim3(64 * NW), (uint32_t)lds, s, g);
     return hipGetLastError();
 }
 
 // Two row groups per block when that still gives every CU a block; fewer
 // row groups than CUs get 16-wave blocks (more loads in flight per block).
+// A grouped launch picks the shape from the row groups of all its problems.
 template <bool Q4>
-static hipError_t launch_skinny_shape(hipStream_t s, const float* X, const mvlm_weight* W, float* Y, int M, int N,
-                                      int K, int num_cus, const Epilogue& ep) {
-    const int groups = (N + 15) / 16;
-    if (groups >= 2 * num_cus) return launch_skinny<Q4, 2, 8>(s, X, W, Y, M, N, K, ep);
-    if (groups >= num_cus) return launch_skinny<Q4, 1, 8>(s, X, W, Y, M, N, K, ep);
-    return launch_skinny<Q4, 1, 16>(s, X, W, Y, M, N, K, ep);
+static hipError_t launch_skinny_shape(hipStream_t s, SkinnyGroup& g, int num_cus) {
+    int groups = 0;
+    for (int i = 0; i < g.count; ++i) groups += (g.p[i].N + 15) / 16;
+    if (groups >= 2 * num_cus) return launch_skinny<Q4, 2, 8>(s, g);
+    if (groups >= num_cus) return launch_skinny<Q4, 1, 8>(s, g);
+    return launch_skinny<Q4, 1, 16>(s, g);
+}
+
+static SkinnyProblem skinny_problem(const float* X, const mvlm_weight* W, float* Y) {
+    SkinnyProblem p{};
+    p.X = X;
+    p.codes = (const uint8_t*)W->data;
+    p.scales = (const uint16_t*)W->scales;
+    p.Y = Y;
+    p.ld = (int64_t)W->ld;
+    p.N = W->N;
+    p.K = W->K;
+    return p;
 }
 
 hipError_t launch_gemm_skinny(hipStream_t s, const float* X, const mvlm_weight* W, float* Y, int M, int N, int K,
                               int num_cus, const Epilogue* ep) {
-    if (M < 1 || M > 16 || K % 32 != 0 || !is_quant(W->dtype)) return hipErrorInvalidValue;
+    if (M < 1 || M > 16 || K % 32 != 0 || !is_quant(W->dtype) || W->N != N || W->K != K) return hipErrorInvalidValue;
     if (num_cus <= 0) num_cus = 256;
-    const Epilogue none{};
-    const Epilogue& e = ep ? *ep : none;
-    if (W->dtype == MVLM_Q4_0) return launch_skinny_shape<true>(s, X, W, Y, M, N, K, num_cus, e);
-    return launch_skinny_shape<false>(s, X, W, Y, M, N, K, num_cus, e);
+    SkinnyGroup g{};
+    g.count = 1;
+    g.M = M;
+    g.p[0] = skinny_problem(X, W, Y);
+    if (ep && ep->any()) {
+        g.p[0].ep = *ep;
+        g.p[0].ep_on = 1;
+    }
+    if (W->dtype == MVLM_Q4_0) return launch_skinny_shape<true>(s, g, num_cus);
+    return launch_skinny_shape<false>(s, g, num_cus);
+}
+
+hipError_t launch_gemm_skinny_group(hipStream_t s, int M, int count, const float* const* Xs,
+                                    const mvlm_weight* const* ws, float* const* Ys, int num_cus) {
+    if (M < 1 || M > 16 || count < 1 || count > SKINNY_MAX_GROUP) return hipErrorInvalidValue;
+    if (num_cus <= 0) num_cus = 256;
+    SkinnyGroup g{};
+    g.count = count;
+    g.M = M;
+    for (int i = 0; i < count; ++i) {
+        const mvlm_weight* W = ws[i];
+        if (W->K % 32 != 0 || !is_quant(W->dtype) || W->dtype != ws[0]->dtype) return hipErrorInvalidValue;
+        g.p[i] = skinny_problem(Xs[i], W, Ys[i]);
+    }
+    if (ws[0]->dtype == MVLM_Q4_0) return launch_skinny_shape<true>(s, g, num_cus);
+    return launch_skinny_shape<false>(s, g, num_cus);
 }
 
 }  // namespace mvlm

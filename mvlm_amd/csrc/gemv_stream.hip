@@ -475,13 +475,16 @@ static hipError_t launch_group_x(hipStream_t s, int x_dtype, StreamGroup& g, siz
 }
 
 // All problems share the weight dtype and x dtype (checked by the caller).
+// M > 1 (2..4 rows of fp32 x per problem, quantized weights) uses the
+// batched-x kernel.
 hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const* xs, int x_dtype,
                                     const mvlm_weight* const* ws, void* const* ys, const int* y_dtypes, int num_cus,
-                                    const Epilogue* eps) {
-    if (count < 1 || count > MAX_GROUP) return hipErrorInvalidValue;
+                                    const Epilogue* eps, int M) {
+    if (count < 1 || count > MAX_GROUP || M < 1 || M > 4) return hipErrorInvalidValue;
     StreamGroup g{};
     g.count = count;
     const int dtype = ws[0]->dtype;
+    if (M > 1 && (!is_quant(dtype) || x_dtype != MVLM_F32)) return hipErrorInvalidValue;
     size_t lds = 0;
     for (int i = 0; i < count; ++i) {
         const mvlm_weight* w = ws[i];
@@ -494,18 +497,19 @@ hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const*
         p.N = w->N;
         p.K = w->K;
         p.y_dtype = y_dtypes[i];
-        p.M = 1;
+        p.M = M;
         p.shape = stream_shape(w);
         if (eps && eps[i].any()) {
             p.ep = eps[i];
             p.ep_on = 1;
         }
-        if (p.shape < 0) return hipErrorInvalidValue;
-        const size_t b = stream_lds_bytes(w, x_dtype, p.shape);
+        if (p.shape < 0 || w->dtype != dtype || (M > 1 && y_dtypes[i] != MVLM_F32)) return hipErrorInvalidValue;
+        const size_t b = stream_lds_bytes(w, x_dtype, p.shape, M > 1 ? 4 : 1);
         lds = b > lds ? b : lds;
     }
     if (lds > STREAM_LDS_MAX) return hipErrorInvalidValue;
     (void)num_cus;
+    if (M > 1) return dtype == MVLM_Q8_0 ? launch_group<Q8Fmt, float, 4>(s, g, lds) : launch_group<Q4Fmt, float, 4>(s, g, lds);
     switch (dtype) {
         case MVLM_Q8_0: return launch_group<Q8Fmt, float>(s, g, lds);
         case MVLM_Q4_0: return launch_group<Q4Fmt, float>(s, g, lds);

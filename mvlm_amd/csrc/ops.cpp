@@ -237,22 +237,27 @@ int make_gemv(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, const mvlm_we
     return MVLM_OK;
 }
 
-int make_gemv_group(mvlm_device* dev, int count, const mvlm_gemv_desc* descs, const char* fn, Op* op) {
+// Independent GEMVs (M = 1) or skinny GEMMs over quantized weights (M <= 16,
+// fp32 x [M][K] and y [M][N] per entry) issued as one launch.
+int make_gemv_group(mvlm_device* dev, int M, int count, const mvlm_gemv_desc* descs, const char* fn, Op* op) {
     REQUIRE(dev && descs, "%s: null argument", fn);
     REQUIRE(count >= 1 && count <= MVLM_MAX_GROUP, "%s: count=%d outside [1, %d]", fn, count, MVLM_MAX_GROUP);
+    REQUIRE(M >= 1 && M <= 16, "%s: M=%d outside [1, 16]", fn, M);
     for (int i = 0; i < count; ++i) {
         const mvlm_gemv_desc& d = descs[i];
         REQUIRE(d.W, "%s: entry %d has no weight", fn, i);
         Op one{};
-        int st = make_gemv(dev, d.x, d.x_dtype, d.W, d.y, d.y_dtype, 1, d.W->N, d.W->K, -1, fn, &one);
+        int st = make_gemv(dev, d.x, d.x_dtype, d.W, d.y, d.y_dtype, M, d.W->N, d.W->K, -1, fn, &one);
         if (st != MVLM_OK) return st;
         REQUIRE(d.W->dtype == descs[0].W->dtype, "%s: entry %d weight dtype %d differs from entry 0 (%d)", fn, i,
                 d.W->dtype, descs[0].W->dtype);
         REQUIRE(d.x_dtype == descs[0].x_dtype, "%s: entry %d x dtype differs from entry 0", fn, i);
-        if (!stream_supported(d.W))
+        if (M == 1 && !stream_supported(d.W))
             return set_error(MVLM_ERR_UNSUPPORTED, "%s: entry %d: rows of %lld bytes (K=%d) are outside the grouped "
                              "kernel's range (<= 16 KiB, K a multiple of the 16-byte vector)", fn, i,
                              (long long)weight_row_bytes(d.W), d.W->K);
+        if (M > 1 && d.W->K % 32 != 0)
+            return set_error(MVLM_ERR_UNSUPPORTED, "%s: entry %d: K=%d is not a multiple of 32", fn, i, d.W->K);
         op->gx[i] = d.x->ptr;
         op->gw[i] = d.W;
         op->gy[i] = d.y->ptr;
@@ -260,15 +265,34 @@ int make_gemv_group(mvlm_device* dev, int count, const mvlm_gemv_desc* descs, co
     }
     op->kind = OP_GEMV_GROUP;
     op->gcount = count;
+    op->M = M;
     op->a_dtype = descs[0].x_dtype;
     op->num_cus = dev->prop.multiProcessorCount;
     return MVLM_OK;
 }
 
+// M > 1: the streaming kernel while every entry fits it (M <= 4), else the
+// matrix-core skinny kernel.
+static hipError_t launch_group_op(hipStream_t s, const Op& op) {
+    if (op.M == 1) return launch_gemv_stream_group(s, op.gcount, op.gx, op.a_dtype, op.gw, op.gy, op.gyd, op.num_cus);
+    bool stream = op.M <= 4;
+    for (int i = 0; i < op.gcount && stream; ++i) stream = stream_supported(op.gw[i], op.M);
+    if (stream)
+        return launch_gemv_stream_group(s, op.gcount, op.gx, op.a_dtype, op.gw, op.gy, op.gyd, op.num_cus, nullptr,
+                                        op.M);
+    const float* xs[MVLM_MAX_GROUP];
+    float* ys[MVLM_MAX_GROUP];
+    for (int i = 0; i < op.gcount; ++i) {
+        xs[i] = (const float*)op.gx[i];
+        ys[i] = (float*)op.gy[i];
+    }
+    return launch_gemm_skinny_group(s, op.M, op.gcount, xs, op.gw, ys, op.num_cus);
+}
+
 hipError_t enqueue_op(hipStream_t s, const Op& op) {
     switch (op.kind) {
         case OP_GEMV_GROUP:
-            return launch_gemv_stream_group(s, op.gcount, op.gx, op.a_dtype, op.gw, op.gy, op.gyd, op.num_cus);
+            return launch_group_op(s, op);
         case OP_GEMM_NAIVE:
             return launch_gemm_naive(s, (const uint16_t*)op.a, (const uint16_t*)op.b, (uint16_t*)op.c, op.M, op.N, op.K);
         case OP_GEMM_TILED:
@@ -374,7 +398,13 @@ extern "C" int mvlm_gemv_ex(mvlm_device* dev, const mvlm_buffer* x, int x_dtype,
 
 extern "C" int mvlm_gemv_grouped(mvlm_device* dev, int count, const mvlm_gemv_desc* descs, mvlm_event** ev) {
     const char* fn = __func__;
-    RUN(make_gemv_group(dev, count, descs, fn, &op));
+    RUN(make_gemv_group(dev, 1, count, descs, fn, &op));
+}
+
+extern "C" int mvlm_gemm_quant_grouped(mvlm_device* dev, int M, int count, const mvlm_gemv_desc* descs,
+                                       mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(make_gemv_group(dev, M, count, descs, fn, &op));
 }
 
 extern "C" int mvlm_gemv_q8_0(mvlm_device* dev, const mvlm_buffer* x, const mvlm_weight* W, mvlm_buffer* y,
@@ -510,7 +540,15 @@ extern "C" int mvlm_plan_add_gemv_grouped(mvlm_plan* plan, int count, const mvlm
     const char* fn = __func__;
     REQUIRE(plan, "%s: null argument", fn);
     Op op{};
-    int st = make_gemv_group(plan->dev, count, descs, fn, &op);
+    int st = make_gemv_group(plan->dev, 1, count, descs, fn, &op);
+    return st != MVLM_OK ? st : plan_push(plan, op);
+}
+
+extern "C" int mvlm_plan_add_gemm_quant_grouped(mvlm_plan* plan, int M, int count, const mvlm_gemv_desc* descs) {
+    const char* fn = __func__;
+    REQUIRE(plan, "%s: null argument", fn);
+    Op op{};
+    int st = make_gemv_group(plan->dev, M, count, descs, fn, &op);
     return st != MVLM_OK ? st : plan_push(plan, op);
 }
 

@@ -106,6 +106,8 @@ _SIGNATURES = {
     "mvlm_plan_add_gemv_ex": (c_int, [_P, _P, c_int, _P, _P, c_int, POINTER(Epilogue)]),
     "mvlm_plan_add_gemm_packed_ex": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, POINTER(Epilogue)]),
     "mvlm_plan_add_gemv_grouped": (c_int, [_P, c_int, POINTER(GemvDesc)]),
+    "mvlm_gemm_quant_grouped": (c_int, [_P, c_int, c_int, POINTER(GemvDesc), _PP]),
+    "mvlm_plan_add_gemm_quant_grouped": (c_int, [_P, c_int, c_int, POINTER(GemvDesc)]),
     "mvlm_gemv_q8_0": (c_int, [_P, _P, _P, _P, c_int, c_int, _PP]),
     "mvlm_gemv_q4_0": (c_int, [_P, _P, _P, _P, c_int, c_int, _PP]),
     "mvlm_gemm_q8_0": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _PP]),
@@ -404,6 +406,14 @@ class Plan:
             self._keep += [x, W, y]
         return self
 
+    def add_gemm_quant_grouped(self, M, entries):
+        """entries: [(X, F32, W, Y, F32), ...] of M-row products over Q8_0 / Q4_0 weights, one launch."""
+        arr = _descs(entries)
+        _call("mvlm_plan_add_gemm_quant_grouped", self.handle, M, len(entries), arr)
+        for x, _, W, y, _ in entries:
+            self._keep += [x, W, y]
+        return self
+
     def add_gemv_ex(self, x, x_dtype, W, y, y_dtype, bias=None, act=ACT_NONE, mul=None, residual=None):
         ep = _epilogue(bias, act, mul, residual)
         _call("mvlm_plan_add_gemv_ex", self.handle, x.handle, x_dtype, W.handle, y.handle, y_dtype, byref(ep))
@@ -562,6 +572,10 @@ class Device:
     def gemv_grouped(self, entries, event=False):
         """entries: [(x, x_dtype, W, y, y_dtype), ...], one launch for all."""
         return self._launch("mvlm_gemv_grouped", (len(entries), _descs(entries)), event)
+
+    def gemm_quant_grouped(self, M, entries, event=False):
+        """entries: [(X, F32, W, Y, F32), ...]: Y = X W^T for each, M rows, one launch."""
+        return self._launch("mvlm_gemm_quant_grouped", (M, len(entries), _descs(entries)), event)
 
     def gemv_q8_0(self, x, W, y, N, K, event=False):
         return self._launch("mvlm_gemv_q8_0", (x.handle, W.handle, y.handle, N, K), event)

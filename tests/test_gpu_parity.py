@@ -419,6 +419,56 @@ def test_gemv_grouped_phi_block(dev, orc, qt):
         assert ok, (N, K, worst)
 
 
+@pytest.mark.parametrize("qt", [Q8, Q4])
+@pytest.mark.parametrize("M", [2, 4, 5, 16])
+def test_gemm_quant_grouped(dev, orc, qt, M):
+    """M rows of activations through a grouped launch (two groups shaped like a
+    Phi-1.5 block's, smaller N): M <= 4 runs the streaming kernel (same bits as
+    the single-op launches), M > 4 the matrix-core skinny kernel"""
+    shapes = [(1536, 2048, 0), (2048, 2048, 0), (512, 2048, 1), (512, 8192, 2)]
+    xs_host = [orc.normal_f32(M * 2048, 261), orc.normal_f32(M * 2048, 262), orc.normal_f32(M * 8192, 263)]
+    xs = [dev.upload(v) for v in xs_host]
+    blocks = [make_quant(orc, qt, N, K, 264 + i) for i, (N, K, _) in enumerate(shapes)]
+    Ws = [dev.pack(b, qt, N, K) for b, (N, K, _) in zip(blocks, shapes)]
+    ys = [dev.alloc(M * N * 4) for N, _, _ in shapes]
+    dev.gemm_quant_grouped(M, [(xs[xi], F32, W, y, F32) for (N, K, xi), W, y in zip(shapes[:2], Ws[:2], ys[:2])])
+    plan = m.Plan(dev)
+    plan.add_gemm_quant_grouped(M, [(xs[xi], F32, W, y, F32) for (N, K, xi), W, y in zip(shapes[2:], Ws[2:], ys[2:])])
+    plan.use_graph(True)
+    plan.run(2)
+    dev.sync()
+    kind = "q8_0" if qt == Q8 else "q4_0"
+    deq = orc.dequant_q8_0 if qt == Q8 else orc.dequant_q4_0
+    single = dev.gemm_q8_0 if qt == Q8 else dev.gemm_q4_0
+    for (N, K, xi), W, b, y in zip(shapes, Ws, blocks, ys):
+        got = y.download(np.float32).reshape(M, N)
+        if M <= 4:
+            y1 = dev.alloc(M * N * 4)
+            single(xs[xi], W, y1, M, N, K)
+            assert np.array_equal(got, y1.download(np.float32).reshape(M, N))
+        X = xs_host[xi].reshape(M, K)
+        ref = orc.gemm_nk(kind, X.ravel(), b, M, N, K)
+        _, S = orc.gemm_f64(X.astype(np.float64), deq(b).astype(np.float64).reshape(N, K), M, N, K)
+        ok, worst = within(got, ref.reshape(M, N), S.reshape(M, N), 1e-5)
+        assert ok, (M, N, K, worst)
+
+
+def test_gemm_quant_grouped_errors(dev):
+    from mvlm_amd import native
+    x, y = dev.alloc(4 * 65536), dev.alloc(4 * 65536)
+    W8 = dev.pack(np.zeros(34 * 64, np.uint8), Q8, 64, 1024)
+    W4 = dev.pack(np.zeros(18 * 64, np.uint8), Q4, 64, 1024)
+    Wh = dev.pack(np.zeros(64 * 1024, np.uint16), F16, 64, 1024)
+    for M, entries, code in ((4, [(x, F32, W8, y, F32), (x, F32, W4, y, F32)], native.ERR_INVALID_ARG),
+                             (0, [(x, F32, W8, y, F32)], native.ERR_INVALID_ARG),
+                             (17, [(x, F32, W8, y, F32)], native.ERR_INVALID_ARG),
+                             (2, [(x, F16, Wh, y, F32)], native.ERR_INVALID_ARG),       # dense weights: M == 1
+                             (8, [(x, F16, W8, y, F32)], native.ERR_INVALID_ARG)):      # fp32 x for quant
+        with pytest.raises(native.MvlmError) as e:
+            dev.gemm_quant_grouped(M, entries)
+        assert e.value.code == code, (M, e.value)
+
+
 def test_gemv_grouped_dense_and_plan(dev, orc):
     shapes = [(300, 512), (77, 1024), (1, 64)]
     xs_host = [orc.normal_f16(K, 201 + i) for i, (_, K) in enumerate(shapes)]
