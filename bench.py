@@ -301,10 +301,19 @@ def cpu_baseline(seconds=10.0):
             orc.gemm_nk("q8_0", x2 if K == 2048 else x8, W, 1, N, K, threads)
         reps += 1
     dt = time.perf_counter() - t0
+    # the same sample on one thread, for a third of the time
+    reps1, t1 = 0, time.perf_counter()
+    while time.perf_counter() - t1 < seconds / 3:
+        for W, N, K in layer:
+            orc.gemm_nk("q8_0", x2 if K == 2048 else x8, W, 1, N, K, 1)
+        reps1 += 1
+    dt1 = time.perf_counter() - t1
     return {"value": nbytes * reps / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{reps} passes over one Phi-1.5 layer's 4 Q8_0 GEMVs (QKV, dense, fc1, fc2; "
                       f"{nbytes / 1e6:.1f} MB each pass) in {dt:.1f} s: dequantize each 32-block exactly, "
-                      f"fp32 fma over ascending k, OpenMP over rows"}
+                      f"fp32 fma over ascending k, OpenMP over rows",
+            "single_thread_value": nbytes * reps1 / dt1 / 1e9,
+            "single_thread_sample": f"{reps1} passes of the same layer on 1 thread in {dt1:.1f} s"}
 
 
 # ---------------------------------------------------------------------------
@@ -458,7 +467,7 @@ def main():
     if not args.no_cpu:
         log("[bench] CPU baseline (oracle Q8_0 GEMV on host cores)")
         cpu = cpu_baseline(args.cpu_seconds)
-        log(f"[bench]   {cpu['value']:.2f} GB/s on {cpu['cores']} threads")
+        log(f"[bench]   {cpu['value']:.2f} GB/s on {cpu['cores']} threads, {cpu['single_thread_value']:.2f} GB/s on 1")
     dev.close()
 
     out = {
