@@ -139,6 +139,42 @@ def decode_step(dev, m, qt, M, steps, warmup, graph=True, grouped=True):
     return res
 
 
+def decode_token(dev, m, qt, cache, steps, warmup):
+    """One Phi-1.5 decode step with the path's own ops end to end: per layer the
+    grouped {QKV, fc1} GEMV, attention of the new token against a `cache`-entry
+    fp16 KV cache (32 heads of 64), the grouped {dense, fc2} GEMV; then the LM
+    head and the on-device token pick.  Layer norm, rotary embedding, the KV
+    append and GELU are not part of this path and are left out."""
+    qdt = m.Q8_0 if qt == "q8_0" else m.Q4_0
+    weights = [dev.random_weight(qdt, N, K, SEED ^ (0x100 + i), 0.02) for i, (_, N, K) in enumerate(PHI_STEP)]
+    ln = dev.fill_normal(dev.alloc(2048 * 4), m.F32, 2048, SEED ^ 0x11, 1.0)
+    att = dev.fill_normal(dev.alloc(2048 * 4), m.F32, 2048, SEED ^ 0x12, 1.0)
+    gelu = dev.fill_normal(dev.alloc(8192 * 4), m.F32, 8192, SEED ^ 0x13, 1.0)
+    ys = {name: dev.alloc(N * 4) for name, N, _ in PHI_LAYER + [PHI_LM_HEAD]}
+    H, D = 32, 64
+    q = dev.fill_normal(dev.alloc(H * D * 2), m.F16, H * D, SEED ^ 0x701, 1.0)
+    k = dev.fill_normal(dev.alloc(cache * H * D * 2), m.F16, cache * H * D, SEED ^ 0x702, 1.0)
+    v = dev.fill_normal(dev.alloc(cache * H * D * 2), m.F16, cache * H * D, SEED ^ 0x703, 1.0)
+    o = dev.alloc(H * D * 2)
+    tok = dev.alloc(4)
+    plan = m.Plan(dev)
+    for layer in range(24):
+        w = dict(zip(("qkv", "dense", "fc1", "fc2"), weights[4 * layer: 4 * layer + 4]))
+        plan.add_gemv_grouped([(ln, m.F32, w["qkv"], ys["qkv"], m.F32), (ln, m.F32, w["fc1"], ys["fc1"], m.F32)])
+        plan.add_attention(q, k, v, o, m.F16, 1, cache, H, D, causal=False)
+        plan.add_gemv_grouped([(att, m.F32, w["dense"], ys["dense"], m.F32),
+                               (gelu, m.F32, w["fc2"], ys["fc2"], m.F32)])
+    plan.add_gemv(ln, m.F32, weights[-1], ys["lm_head"], m.F32, 1)
+    plan.add_argmax(ys["lm_head"], m.F32, 1, 51200, 51200, tok)
+    plan.use_graph(True)
+    ms = timed_plan(dev, plan, steps, warmup)
+    plan.destroy()
+    for W in weights:
+        W.free()
+    return {"workload": f"phi15_decode_token_{qt}_cache{cache}", "us": ms * 1e3, "tokens_per_s": 1e3 / ms,
+            "ops": 24 * 3 + 2}
+
+
 def fp32_gemv(dev, m, steps, warmup, copies=16):
     """x[1x2048] . W[2048x8192] fp32 (gemm_bench.cpp's llm_ffn shape), rotating over
     `copies` weight copies (16 x 67 MB > the 256 MB Infinity Cache)."""
@@ -457,6 +493,11 @@ def main():
             extra[r["workload"]] = r
             log(f"[bench]   {r['workload']}: {r['ms_per_step'] * 1e3:.1f} us/step {r['gbs']:.0f} GB/s "
                 f"({100 * r['frac']:.1f}%)")
+        for qt, cache in (("q8_0", 512), ("q8_0", 2048), ("q4_0", 512)):
+            r = decode_token(dev, m, qt, cache, max(10, args.steps // 2), 3)
+            extra[r["workload"]] = r
+            log(f"[bench]   {r['workload']}: {r['us']:.1f} us/token ({r['tokens_per_s']:.0f} tokens/s; GEMVs, "
+                f"attention, LM head and token pick, one graph)")
         r = fp32_gemv(dev, m, max(10, args.steps // 2), 3)
         extra[r["workload"]] = r
         log(f"[bench]   {r['workload']}: {r['us']:.1f} us {r['gbs']:.0f} GB/s ({100 * r['frac']:.1f}%)")
