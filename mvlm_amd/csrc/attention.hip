@@ -413,13 +413,7 @@ static hipError_t launch_variant(hipStream_t s, const AttnArgs& a) {
     auto kernel = attention_kernel<KS, DT, NW>;
     constexpr int lds = NW * AttnLayout<KS, DT>::REGION;
     static_assert(lds <= ATTN_LDS_MAX, "attention LDS over budget");
-    static bool attr_set = false;
-    if (!attr_set) {
-        const hipError_t e =
-            hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, ATTN_LDS_MAX);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    if (const hipError_t e = allow_dynamic_lds<attention_kernel<KS, DT, NW>>(ATTN_LDS_MAX); e != hipSuccess) return e;
     const dim3 grid((unsigned)((a.seq_q + 31) / 32), (unsigned)a.heads, (unsigned)a.splits);
     if (a.splits == 1) {
         launch_kernel(kernel, grid, dim3(64 * NW), (uint32_t)lds, s, a);

@@ -132,6 +132,15 @@ inline void launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint3
 }
 
 // An op made of two dependent kernels: the first carries the start event and
+// Raises kernel Kernel's dynamic LDS limit to `bytes`, once per process (a
+// thread-safe function-local static per kernel); returns that call's status.
+template <auto Kernel>
+inline hipError_t allow_dynamic_lds(int bytes) {
+    static const hipError_t status =
+        hipFuncSetAttribute((const void*)Kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    return status;
+}
+
 // the second the stop event, so plan profiling times the pair.
 enum class LaunchPart { First, Last };
 template <typename... KArgs, typename... Args>

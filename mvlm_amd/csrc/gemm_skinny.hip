@@ -322,13 +322,8 @@ static hipError_t launch_skinny(hipStream_t s, SkinnyGroup& g) {
         g.p[i].block_begin = (int)blocks;
         blocks += (unsigned)((g.p[i].N + 16 * R - 1) / (16 * R));
     }
-    static bool attr_set = false;
-    if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)SKINNY_LDS_MAX);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    if (const hipError_t e = allow_dynamic_lds<gemm_skinny_kernel<Q4, R, NW>>((int)SKINNY_LDS_MAX); e != hipSuccess)
+        return e;
     if (lds > SKINNY_LDS_MAX) return hipErrorInvalidValue;
     launch_kernel(kernel, dim3(blocks), dim3(64 * NW), (uint32_t)lds, s, g);
     return hipGetLastError();

@@ -452,13 +452,8 @@ static unsigned partition(StreamGroup& g) {
 template <class F, typename XT, int MX = 1>
 static hipError_t launch_group(hipStream_t s, StreamGroup& g, size_t lds) {
     auto kernel = gemv_stream_kernel<F, XT, MX>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)STREAM_LDS_MAX);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    if (const hipError_t e = allow_dynamic_lds<gemv_stream_kernel<F, XT, MX>>((int)STREAM_LDS_MAX); e != hipSuccess)
+        return e;
     const unsigned blocks = partition(g);
     launch_kernel(kernel, dim3(blocks), dim3(64 * NWAVE), (uint32_t)lds, s, g);
     return hipGetLastError();
