@@ -499,13 +499,17 @@ static hipError_t launch_dims(hipStream_t s, const AttnArgs& a, int num_cus) {
 
 hipError_t launch_attention(hipStream_t s, const void* Q, const void* K, const void* V, void* O, int o_dtype,
                             int seq_q, int seq_kv, int heads, int head_dim, int causal, float scale, int num_cus,
-                            void* workspace) {
+                            void* workspace, size_t workspace_bytes) {
     AttnArgs a{};
     a.splits = pick_splits(seq_q, seq_kv, heads, num_cus);
     const int tiles = (seq_kv + 31) / 32;
     a.tiles_per_split = (tiles + a.splits - 1) / a.splits;
     a.ws = (float*)workspace;
-    if (a.splits > 1 && !workspace) return hipErrorInvalidValue;
+    // the split count is re-chosen here; a workspace sized for fewer splits
+    // (MVLM_ATTN_SPLITS changed after the op was made) is refused
+    if (a.splits > 1 &&
+        (!workspace || workspace_bytes < (size_t)a.splits * seq_q * heads * (head_dim + 2) * sizeof(float)))
+        return hipErrorInvalidValue;
     a.Q = (const uint16_t*)Q; a.K = (const uint16_t*)K; a.V = (const uint16_t*)V; a.O = O;
     a.o_dtype = o_dtype;
     a.seq_q = seq_q; a.seq_kv = seq_kv; a.heads = heads; a.D = head_dim;

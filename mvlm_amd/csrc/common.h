@@ -208,7 +208,7 @@ hipError_t launch_gemm_mfma(hipStream_t s, const void* A, int ab_dtype, const vo
 size_t attention_workspace_bytes(int seq_q, int seq_kv, int heads, int head_dim, int num_cus);
 hipError_t launch_attention(hipStream_t s, const void* Q, const void* K, const void* V, void* O, int o_dtype,
                             int seq_q, int seq_kv, int heads, int head_dim, int causal, float scale, int num_cus,
-                            void* workspace);
+                            void* workspace, size_t workspace_bytes);
 // row-wise argmax (first index of the largest key), one workgroup per row
 hipError_t launch_argmax(hipStream_t s, const void* x, int dtype, int rows, int n, int64_t ld, int* out);
 hipError_t launch_pack(hipStream_t s, const void* src, int dtype, int layout, int N, int K,

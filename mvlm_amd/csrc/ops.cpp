@@ -185,8 +185,8 @@ int make_attention(mvlm_device* dev, const mvlm_buffer* Q, const mvlm_buffer* K,
     op->causal = causal ? 1 : 0;
     op->scale = scale == 0.0f ? 1.0f / sqrtf((float)head_dim) : scale;
     op->num_cus = dev->prop.multiProcessorCount;
-    return device_scratch(dev, attention_workspace_bytes(seq_q, seq_kv, heads, head_dim, op->num_cus),
-                          &op->workspace);
+    op->workspace_bytes = attention_workspace_bytes(seq_q, seq_kv, heads, head_dim, op->num_cus);
+    return device_scratch(dev, op->workspace_bytes, &op->workspace);
 }
 
 int make_argmax(mvlm_device* dev, const mvlm_buffer* x, int dtype, int rows, int n, int64_t ld,
@@ -316,7 +316,7 @@ hipError_t enqueue_op(hipStream_t s, const Op& op) {
             return launch_argmax(s, op.a, op.a_dtype, op.M, op.N, op.lda, (int*)op.c);
         case OP_ATTENTION:
             return launch_attention(s, op.a, op.b, op.v, op.c, op.c_dtype, op.M, op.N, op.batch, op.K, op.causal,
-                                    op.scale, op.num_cus, op.workspace);
+                                    op.scale, op.num_cus, op.workspace, op.workspace_bytes);
     }
     return hipErrorInvalidValue;
 }

@@ -105,6 +105,26 @@ def test_attention_forced_waves_with_key_splits(dev, orc, monkeypatch, waves, sp
     run(dev, orc, 40, 300, 4, 72, True, F16, seed=42)
 
 
+def test_attention_split_override_after_planning_is_refused(dev, monkeypatch):
+    """a plan entry sized for one split (no workspace) must not launch with more
+    splits when MVLM_ATTN_SPLITS changes afterwards: the launch is refused on
+    the host"""
+    from mvlm_amd import native
+    H, D, S = 8, 64, 512
+    q, k, v = dev.alloc(H * D * 2), dev.alloc(S * H * D * 2), dev.alloc(S * H * D * 2)
+    o = dev.alloc(H * D * 4)
+    monkeypatch.delenv("MVLM_ATTN_SPLITS", raising=False)
+    plan = m.Plan(dev)
+    plan.add_attention(q, k, v, o, F32, 1, S, H, D, causal=False)
+    plan.run(1)
+    dev.sync()
+    monkeypatch.setenv("MVLM_ATTN_SPLITS", "4")
+    with pytest.raises(native.MvlmError):
+        plan.run(1)
+    dev.sync()
+    plan.destroy()
+
+
 def test_attention_long_cache_single_block(dev, orc, monkeypatch):
     """a 2048-entry cache without key splits: 16 waves per (head) block, 4 key
     tiles each, merged in LDS"""
