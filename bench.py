@@ -418,10 +418,10 @@ def pmc_summarize(fetch_dir, write_dir, out=TRAFFIC_FILE):
     summary = {"workload": "phi15_decode_q8_0", "algorithmic_bytes_per_step": alg,
                "hbm_bytes_per_step": total, "ratio_to_algorithmic": total / alg, "fetch": res["fetch"],
                "write": res["write"],
-               "command": "cd /tmp && export TMPDIR=/tmp && rocprofv3 --pmc FETCH_SIZE -d $R/gpurun_out/pmc_fetch "
+               "command": "cd /tmp && export TMPDIR=/tmp && rocprofv3 --pmc FETCH_SIZE -d $OUT/pmc_fetch "
                           "-o run --output-format csv -- python3 $R/bench.py --pmc-probe; same with WRITE_SIZE "
-                          "into pmc_write; python3 $R/bench.py --pmc-summarize gpurun_out/pmc_fetch "
-                          "gpurun_out/pmc_write   (R = repository root)"}
+                          "into $OUT/pmc_write; python3 $R/bench.py --pmc-summarize $OUT/pmc_fetch "
+                          "$OUT/pmc_write   (R = repository root, OUT = an output directory)"}
     with open(out, "w") as fh:
         json.dump(summary, fh, indent=1)
     print(json.dumps(summary, indent=1))
@@ -461,8 +461,8 @@ def main():
         pmc_probe()
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the decode GEMV would shard "
-              "along N, see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: this library has no multi-GPU path (the decode GEMV would shard "
+              "along N, each GPU streaming its rows); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import mvlm_amd as m

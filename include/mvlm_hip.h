@@ -39,7 +39,7 @@ enum mvlm_status {
     MVLM_ERR_NO_DEVICE = -2,     /* no HIP device, or ordinal out of range   */
     MVLM_ERR_OUT_OF_MEMORY = -3, /* device or host allocation failed        */
     MVLM_ERR_HIP = -4,           /* a HIP runtime call failed               */
-    MVLM_ERR_UNSUPPORTED = -5,   /* valid request this build does not serve */
+    MVLM_ERR_UNSUPPORTED = -5,   /* valid request this library does not serve */
     MVLM_ERR_BUFFER_TOO_SMALL = -6,
     MVLM_ERR_NOT_FOUND = -7,     /* no such tensor / metadata key            */
     MVLM_ERR_FORMAT = -8         /* malformed or truncated file              */
@@ -163,7 +163,7 @@ int mvlm_gemv(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, const mvlm_we
  * 204-255) and vector_add for residuals (activations.cl:259-290).
  * MVLM_ACT_GELU_TANH is 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), the
  * formula of activations.cl:68 (the kernel there evaluates the tanh with the
- * sign flipped, activations.cl:96-116, which this build does not reproduce).
+ * sign flipped, activations.cl:96-116, which this library does not reproduce).
  * bias ([N]), mul and residual ([M][N], row stride N) are optional, have the
  * output's dtype, and may alias the output. */
 enum mvlm_activation {

@@ -344,7 +344,7 @@ extern "C" int mvlm_weight_from_gguf(mvlm_device* dev, const mvlm_gguf* g, uint6
     REQUIRE(t.dims[0] <= (uint64_t)INT32_MAX && t.dims[1] <= (uint64_t)INT32_MAX,
             "mvlm_weight_from_gguf: dims too large");
     if (!is_dense((int)t.type) && !is_quant((int)t.type))
-        return set_error(MVLM_ERR_UNSUPPORTED, "mvlm_weight_from_gguf: ggml type %u is not packed by this build "
+        return set_error(MVLM_ERR_UNSUPPORTED, "mvlm_weight_from_gguf: ggml type %u is not packed by this library "
                          "(F32, F16, BF16, Q8_0, Q4_0)", t.type);
     const void* data = g->base() + g->info.data_offset + t.offset;
     return mvlm_weight_pack(dev, data, (int)t.type, MVLM_LAYOUT_NK, (int)t.dims[1], (int)t.dims[0], out);
