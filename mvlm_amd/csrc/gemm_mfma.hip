@@ -309,18 +309,32 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(const GemmArg
 }
 
 // Sums the split-K partials in split order (deterministic), applies the
-// epilogue and stores C: thread = one output element.
+// epilogue and stores C: thread = V consecutive output elements of the
+// flattened [M][N] (V = 4 reads the partials as 16-byte vectors; it needs
+// M*N % 4 == 0 so every split's partial stays 16-byte aligned).
+template <int V>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const GemmArgs p) {
     const int64_t mn = (int64_t)p.M * p.N;
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V;
     const int b = blockIdx.y;
-    if (i >= mn) return;
-    const float* ws = p.ws + (int64_t)b * p.splits * mn + i;
-    float v = 0.0f;
-    for (int s = 0; s < p.splits; ++s) v += ws[s * mn];
-    const int row = (int)(i / p.N), col = (int)(i - (int64_t)row * p.N);
-    const int64_t idx = (int64_t)b * p.sC + (int64_t)row * p.ldc + col;
-    store_out(p.C, idx, p.ep_on ? apply_epilogue(p.ep, v, idx, col) : v, p.c_dtype);
+    if (i0 >= mn) return;
+    const float* ws = p.ws + (int64_t)b * p.splits * mn + i0;
+    float v[V];
+    if constexpr (V == 4) {
+        f32x4 acc = *reinterpret_cast<const f32x4*>(ws);
+        for (int s = 1; s < p.splits; ++s) acc += *reinterpret_cast<const f32x4*>(ws + s * mn);
+        v[0] = acc[0]; v[1] = acc[1]; v[2] = acc[2]; v[3] = acc[3];
+    } else {
+        v[0] = 0.0f;
+        for (int s = 0; s < p.splits; ++s) v[0] += ws[s * mn];
+    }
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+        const int64_t i = i0 + e;
+        const int row = (int)(i / p.N), col = (int)(i - (int64_t)row * p.N);
+        const int64_t idx = (int64_t)b * p.sC + (int64_t)row * p.ldc + col;
+        store_out(p.C, idx, p.ep_on ? apply_epilogue(p.ep, v[e], idx, col) : v[e], p.c_dtype);
+    }
 }
 
 // ---- launch configuration ----------------------------------------------------
@@ -442,8 +456,12 @@ hipError_t launch_gemm_mfma(hipStream_t s, const void* A, int ab_dtype, const vo
     }
     launch_kernel_part(LaunchPart::First, k, grid, dim3(64 * t.waves), 0, s, a);
     const int64_t mn = (int64_t)M * N;
-    launch_kernel_part(LaunchPart::Last, gemm_splitk_reduce_kernel, dim3((unsigned)((mn + 255) / 256), (unsigned)batch),
-                       dim3(256), 0, s, a);
+    if (mn % 4 == 0)
+        launch_kernel_part(LaunchPart::Last, gemm_splitk_reduce_kernel<4>,
+                           dim3((unsigned)((mn / 4 + 255) / 256), (unsigned)batch), dim3(256), 0, s, a);
+    else
+        launch_kernel_part(LaunchPart::Last, gemm_splitk_reduce_kernel<1>,
+                           dim3((unsigned)((mn + 255) / 256), (unsigned)batch), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
