@@ -453,6 +453,28 @@ def test_gemm_quant_grouped(dev, orc, qt, M):
         assert ok, (M, N, K, worst)
 
 
+@pytest.mark.parametrize("qt", [Q8, Q4])
+@pytest.mark.parametrize("M", [3, 7])
+def test_gemm_quant_grouped_ragged(dev, orc, qt, M):
+    """ragged row counts (not multiples of the 16-row tile or of the block's
+    rows) and different K in one group: blocks are dealt to the problems in
+    order and each block stages its own problem's K"""
+    shapes = [(17, 96), (300, 2048), (33, 1024), (1, 32), (129, 8192)]
+    kind = "q8_0" if qt == Q8 else "q4_0"
+    deq = orc.dequant_q8_0 if qt == Q8 else orc.dequant_q4_0
+    Xh = [orc.normal_f32(M * K, 281 + i) for i, (_, K) in enumerate(shapes)]
+    blocks = [make_quant(orc, qt, N, K, 291 + i) for i, (N, K) in enumerate(shapes)]
+    Ws = [dev.pack(b, qt, N, K) for b, (N, K) in zip(blocks, shapes)]
+    Xs = [dev.upload(x) for x in Xh]
+    Ys = [dev.alloc(M * N * 4) for N, _ in shapes]
+    dev.gemm_quant_grouped(M, [(x, F32, W, y, F32) for x, W, y in zip(Xs, Ws, Ys)])
+    for (N, K), x, b, y in zip(shapes, Xh, blocks, Ys):
+        ref = orc.gemm_nk(kind, x, b, M, N, K)
+        _, S = orc.gemm_f64(x.astype(np.float64).reshape(M, K), deq(b).astype(np.float64).reshape(N, K), M, N, K)
+        ok, worst = within(y.download(np.float32).reshape(M, N), ref.reshape(M, N), S.reshape(M, N), 1e-5)
+        assert ok, (M, N, K, worst)
+
+
 def test_gemm_quant_grouped_errors(dev):
     from mvlm_amd import native
     x, y = dev.alloc(4 * 65536), dev.alloc(4 * 65536)
