@@ -238,14 +238,18 @@ int make_gemv(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, const mvlm_we
 }
 
 // Independent GEMVs (M = 1) or skinny GEMMs over quantized weights (M <= 16,
-// fp32 x [M][K] and y [M][N] per entry) issued as one launch.
-int make_gemv_group(mvlm_device* dev, int M, int count, const mvlm_gemv_desc* descs, const char* fn, Op* op) {
+// fp32 x [M][K] and y [M][N] per entry) issued as one launch; quant_only
+// refuses dense weights at M = 1 too.
+int make_gemv_group(mvlm_device* dev, int M, int count, const mvlm_gemv_desc* descs, const char* fn, Op* op,
+                    bool quant_only = false) {
     REQUIRE(dev && descs, "%s: null argument", fn);
     REQUIRE(count >= 1 && count <= MVLM_MAX_GROUP, "%s: count=%d outside [1, %d]", fn, count, MVLM_MAX_GROUP);
     REQUIRE(M >= 1 && M <= 16, "%s: M=%d outside [1, 16]", fn, M);
     for (int i = 0; i < count; ++i) {
         const mvlm_gemv_desc& d = descs[i];
         REQUIRE(d.W, "%s: entry %d has no weight", fn, i);
+        REQUIRE(!quant_only || is_quant(d.W->dtype), "%s: entry %d weight dtype %d is not Q8_0/Q4_0", fn, i,
+                d.W->dtype);
         Op one{};
         int st = make_gemv(dev, d.x, d.x_dtype, d.W, d.y, d.y_dtype, M, d.W->N, d.W->K, -1, fn, &one);
         if (st != MVLM_OK) return st;
@@ -404,7 +408,7 @@ extern "C" int mvlm_gemv_grouped(mvlm_device* dev, int count, const mvlm_gemv_de
 extern "C" int mvlm_gemm_quant_grouped(mvlm_device* dev, int M, int count, const mvlm_gemv_desc* descs,
                                        mvlm_event** ev) {
     const char* fn = __func__;
-    RUN(make_gemv_group(dev, M, count, descs, fn, &op));
+    RUN(make_gemv_group(dev, M, count, descs, fn, &op, true));
 }
 
 extern "C" int mvlm_gemv_q8_0(mvlm_device* dev, const mvlm_buffer* x, const mvlm_weight* W, mvlm_buffer* y,
@@ -548,7 +552,7 @@ extern "C" int mvlm_plan_add_gemm_quant_grouped(mvlm_plan* plan, int M, int coun
     const char* fn = __func__;
     REQUIRE(plan, "%s: null argument", fn);
     Op op{};
-    int st = make_gemv_group(plan->dev, M, count, descs, fn, &op);
+    int st = make_gemv_group(plan->dev, M, count, descs, fn, &op, true);
     return st != MVLM_OK ? st : plan_push(plan, op);
 }
 

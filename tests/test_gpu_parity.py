@@ -484,7 +484,8 @@ def test_gemm_quant_grouped_errors(dev):
     for M, entries, code in ((4, [(x, F32, W8, y, F32), (x, F32, W4, y, F32)], native.ERR_INVALID_ARG),
                              (0, [(x, F32, W8, y, F32)], native.ERR_INVALID_ARG),
                              (17, [(x, F32, W8, y, F32)], native.ERR_INVALID_ARG),
-                             (2, [(x, F16, Wh, y, F32)], native.ERR_INVALID_ARG),       # dense weights: M == 1
+                             (2, [(x, F16, Wh, y, F32)], native.ERR_INVALID_ARG),       # dense weights
+                             (1, [(x, F16, Wh, y, F32)], native.ERR_INVALID_ARG),       # also at M == 1
                              (8, [(x, F16, W8, y, F32)], native.ERR_INVALID_ARG)):      # fp32 x for quant
         with pytest.raises(native.MvlmError) as e:
             dev.gemm_quant_grouped(M, entries)
