@@ -196,6 +196,27 @@ def fp32_gemv(dev, m, steps, warmup, copies=16):
     return res
 
 
+def gemv_exact(dev, m, steps, warmup, copies=16):
+    """mvlm_gemv_exact (the reference gemv's summation order, fp16 in and out) at
+    x[1x2048] . W[2048x8192], rotating over `copies` 32 MB packed fp16 weights."""
+    N, K = 8192, 2048
+    Bs = [dev.random_weight(m.F16, N, K, SEED ^ (0x300 + i), 0.02) for i in range(copies)]
+    x = dev.fill_normal(dev.alloc(K * 2), m.F16, K, SEED ^ 0x301, 1.0)
+    y = dev.alloc(N * 2)
+    for i in range(warmup):
+        dev.gemv_exact(x, Bs[i % copies], y, N, K)
+    dev.sync()
+    times = []
+    for i in range(max(steps, copies)):
+        ev = dev.gemv_exact(x, Bs[i % copies], y, N, K, event=True)
+        ev.wait()
+        times.append(ev.elapsed_ms())
+    us = float(np.median(times)) * 1e3
+    nbytes = 2.0 * N * K + 2 * K + 2 * N
+    return {"workload": "gemv_exact_f16_2048x8192", "kernel_us": us, "gbs": nbytes / us / 1e3,
+            "frac": nbytes / us / 1e3 / PEAK_HBM_GBS}
+
+
 def gemm_shape(dev, m, name, M, N, K, steps, warmup):
     """fp16-in / fp32-out MFMA GEMM, A[M,K] N(0,1), W[N,K] N(0,0.02)."""
     W = dev.random_weight(m.F16, N, K, SEED ^ (zlib.crc32(name.encode()) & 0xFFFF), 0.02)
@@ -501,6 +522,10 @@ def main():
         r = fp32_gemv(dev, m, max(10, args.steps // 2), 3)
         extra[r["workload"]] = r
         log(f"[bench]   {r['workload']}: {r['us']:.1f} us {r['gbs']:.0f} GB/s ({100 * r['frac']:.1f}%)")
+        r = gemv_exact(dev, m, 32, 4)
+        extra[r["workload"]] = r
+        log(f"[bench]   {r['workload']}: {r['kernel_us']:.1f} us kernel {r['gbs']:.0f} GB/s "
+            f"({100 * r['frac']:.1f}%; reference summation order)")
         gemm_extras(dev, m, 20, 5, extra)
         f4_extras(dev, m, 20, 5, extra)
 

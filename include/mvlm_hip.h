@@ -152,6 +152,14 @@ int mvlm_gemm_packed(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, const 
  * y_dtype F32, F16 or BF16.  fp32 accumulation. */
 int mvlm_gemv(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W,
               mvlm_buffer* y, int y_dtype, int N, int K, mvlm_event** ev);
+/* dispatch_gemv (compute.cpp:122-152) with the arithmetic of gemv
+ * (gemm.cl:215-270): y[N] = x[K] * W for a packed F16 weight, fp16 x (8-byte
+ * aligned) and fp16 y; each output is 256 fp32 fma partials over
+ * k = L, L+256, ..., folded pairwise over strides 128..1 and stored
+ * round-to-nearest-even, so y is bit-identical to the reference's.
+ * mvlm_gemv is the faster path for the same product. */
+int mvlm_gemv_exact(mvlm_device* dev, const mvlm_buffer* x, const mvlm_weight* W, mvlm_buffer* y,
+                    int N, int K, mvlm_event** ev);
 
 /* ---- fused epilogues ----------------------------------------------------------
  * out = act(acc + bias[n]) * mul[m][n] + residual[m][n], applied to the fp32

@@ -173,6 +173,9 @@ hipError_t launch_gemm_naive(hipStream_t s, const uint16_t* A, const uint16_t* B
                              int M, int N, int K);
 hipError_t launch_gemm_tiled(hipStream_t s, const uint16_t* A, const uint16_t* B, uint16_t* C,
                              int M, int N, int K);
+// y[N] = W[N,K] x[K], packed fp16 W, fp16 x and y, the reference gemv's
+// summation order (x 8-byte aligned)
+hipError_t launch_gemv_exact(hipStream_t s, const uint16_t* x, const mvlm_weight* W, uint16_t* y);
 hipError_t launch_gemv_dense(hipStream_t s, const void* x, int x_dtype, const mvlm_weight* W,
                              void* y, int y_dtype, int N, int K);
 // Q8_0 / Q4_0 skinny GEMM on the matrix cores, 1 <= M <= 16 (any row length)

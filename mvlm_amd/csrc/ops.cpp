@@ -16,7 +16,7 @@ using namespace mvlm;
 
 namespace {
 
-enum OpKind { OP_GEMM_NAIVE, OP_GEMM_TILED, OP_GEMM_MFMA, OP_GEMV_DENSE, OP_GEMV_QUANT, OP_GEMV_GROUP, OP_ATTENTION, OP_ARGMAX };
+enum OpKind { OP_GEMM_NAIVE, OP_GEMM_TILED, OP_GEMV_EXACT, OP_GEMM_MFMA, OP_GEMV_DENSE, OP_GEMV_QUANT, OP_GEMV_GROUP, OP_ATTENTION, OP_ARGMAX };
 
 struct Op {
     OpKind kind;
@@ -97,6 +97,22 @@ int make_ref_gemm(OpKind kind, mvlm_device* dev, const mvlm_buffer* A, const mvl
     op->kind = kind;
     op->a = A->ptr; op->b = B->ptr; op->c = C->ptr;
     op->M = M; op->N = N; op->K = K;
+    return MVLM_OK;
+}
+
+int make_gemv_exact(mvlm_device* dev, const mvlm_buffer* x, const mvlm_weight* W, mvlm_buffer* y, int N, int K,
+                    const char* fn, Op* op) {
+    REQUIRE(dev && x && W && y, "%s: null argument", fn);
+    REQUIRE(x->dev == dev && W->dev == dev && y->dev == dev, "%s: handles belong to another device", fn);
+    REQUIRE(N > 0 && K > 0, "%s: N=%d K=%d must be positive", fn, N, K);
+    REQUIRE(W->N == N && W->K == K, "%s: weight is [%d x %d], call asks for N=%d K=%d", fn, W->N, W->K, N, K);
+    REQUIRE(W->dtype == MVLM_F16, "%s: weight dtype %d is not F16", fn, W->dtype);
+    REQUIRE(((uintptr_t)x->ptr & 7u) == 0, "%s: x must be 8-byte aligned", fn);
+    NEED(x, (size_t)K * 2, "x");
+    NEED(y, (size_t)N * 2, "y");
+    op->kind = OP_GEMV_EXACT;
+    op->a = x->ptr; op->w = W; op->c = y->ptr;
+    op->M = 1; op->N = N; op->K = K;
     return MVLM_OK;
 }
 
@@ -301,6 +317,8 @@ hipError_t enqueue_op(hipStream_t s, const Op& op) {
             return launch_gemm_naive(s, (const uint16_t*)op.a, (const uint16_t*)op.b, (uint16_t*)op.c, op.M, op.N, op.K);
         case OP_GEMM_TILED:
             return launch_gemm_tiled(s, (const uint16_t*)op.a, (const uint16_t*)op.b, (uint16_t*)op.c, op.M, op.N, op.K);
+        case OP_GEMV_EXACT:
+            return launch_gemv_exact(s, (const uint16_t*)op.a, op.w, (uint16_t*)op.c);
         case OP_GEMM_MFMA:
             return launch_gemm_mfma(s, op.a, op.a_dtype, op.b, op.c, op.c_dtype, op.batch, op.M, op.N, op.K,
                                     op.lda, op.ldb, op.ldc, op.sA, op.sB, op.sC, op.kread_b, op.num_cus, &op.ep,
@@ -364,6 +382,12 @@ extern "C" int mvlm_gemm_tiled(mvlm_device* dev, const mvlm_buffer* A, const mvl
                                int M, int N, int K, mvlm_event** ev) {
     const char* fn = __func__;
     RUN(make_ref_gemm(OP_GEMM_TILED, dev, A, B, C, M, N, K, fn, &op));
+}
+
+extern "C" int mvlm_gemv_exact(mvlm_device* dev, const mvlm_buffer* x, const mvlm_weight* W, mvlm_buffer* y,
+                               int N, int K, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(make_gemv_exact(dev, x, W, y, N, K, fn, &op));
 }
 
 extern "C" int mvlm_gemm_packed(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, const mvlm_weight* W,

@@ -144,6 +144,11 @@ Event dispatch_gemv(const DeviceInfo* dev, Program, Buffer x, Weight W_img, Buff
                                                                                                     : nullptr;
 }
 
+Event dispatch_gemv_exact(const DeviceInfo* dev, Program, Buffer x, Weight W_img, Buffer y, int N, int K) {
+    mvlm_event* ev = nullptr;
+    return dev && ok(mvlm_gemv_exact(dev->device, x, W_img, y, N, K, &ev), "dispatch_gemv_exact") ? ev : nullptr;
+}
+
 Event dispatch_gemv_quant(const DeviceInfo* dev, Program, Buffer x, Weight W, Buffer y, int M, int N, int K) {
     if (!dev || !W) return nullptr;
     mvlm_event* ev = nullptr;

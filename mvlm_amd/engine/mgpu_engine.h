@@ -74,6 +74,8 @@ Event dispatch_gemm_tiled(const DeviceInfo* dev, Program program, Buffer A, Buff
 Event dispatch_gemm_image(const DeviceInfo* dev, Program program, Buffer A, Weight B_img, Buffer C, int M, int N, int K);
 // y[1,N] = x[1,K] * W_img; fp16 x and y.
 Event dispatch_gemv(const DeviceInfo* dev, Program program, Buffer x, Weight W_img, Buffer y, int N, int K);
+// Same product with gemv's summation order (gemm.cl:215-270): bit-identical y.
+Event dispatch_gemv_exact(const DeviceInfo* dev, Program program, Buffer x, Weight W_img, Buffer y, int N, int K);
 // The dequantizing GEMV of README.md:57 (fp32 x and y, Q8_0 / Q4_0 weights), M <= 16 rows.
 Event dispatch_gemv_quant(const DeviceInfo* dev, Program program, Buffer x, Weight W, Buffer y, int M, int N, int K);
 // src/engine/compute.h:65-73 (fused MFMA attention; fp16 [seq][heads][head_dim])

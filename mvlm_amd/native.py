@@ -98,6 +98,7 @@ _SIGNATURES = {
     "mvlm_weight_dequant": (c_int, [_P, _P, _P, _PP]),
     "mvlm_gemm_naive": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _PP]),
     "mvlm_gemm_tiled": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _PP]),
+    "mvlm_gemv_exact": (c_int, [_P, _P, _P, _P, c_int, c_int, _PP]),
     "mvlm_gemm_packed": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, c_int, c_int, _PP]),
     "mvlm_gemv": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, c_int, _PP]),
     "mvlm_gemv_grouped": (c_int, [_P, c_int, POINTER(GemvDesc), _PP]),
@@ -551,6 +552,9 @@ class Device:
 
     def gemm_tiled(self, A, B, C, M, N, K, event=False):
         return self._launch("mvlm_gemm_tiled", (A.handle, B.handle, C.handle, M, N, K), event)
+
+    def gemv_exact(self, x, W, y, N, K, event=False):
+        return self._launch("mvlm_gemv_exact", (x.handle, W.handle, y.handle, N, K), event)
 
     def gemm_packed(self, A, a_dtype, W, C, c_dtype, M, N, K, event=False):
         return self._launch("mvlm_gemm_packed", (A.handle, a_dtype, W.handle, C.handle, c_dtype, M, N, K), event)

@@ -21,7 +21,7 @@ def declared_functions():
 
 def test_header_declares_the_boundary():
     names = declared_functions()
-    for must in ["mvlm_gemm_naive", "mvlm_gemm_tiled", "mvlm_gemm_packed", "mvlm_gemv",
+    for must in ["mvlm_gemm_naive", "mvlm_gemm_tiled", "mvlm_gemm_packed", "mvlm_gemv", "mvlm_gemv_exact",
                  "mvlm_gemv_q8_0", "mvlm_gemv_q4_0", "mvlm_gemm_q8_0", "mvlm_gemm_q4_0",
                  "mvlm_gemm_batched", "mvlm_weight_pack", "mvlm_pool_init", "mvlm_device_create",
                  "mvlm_gguf_open", "mvlm_gguf_find_tensor", "mvlm_weight_from_gguf"]:
@@ -67,6 +67,7 @@ def test_null_arguments_are_rejected_on_the_host():
     assert L.mvlm_buffer_alloc(None, 16, ctypes.byref(out)) == native.ERR_INVALID_ARG
     assert L.mvlm_gemm_naive(None, None, None, None, 4, 4, 4, None) == native.ERR_INVALID_ARG
     assert L.mvlm_gemm_tiled(None, None, None, None, 4, 4, 4, None) == native.ERR_INVALID_ARG
+    assert L.mvlm_gemv_exact(None, None, None, None, 4, 4, None) == native.ERR_INVALID_ARG
     assert L.mvlm_gemm_packed(None, None, 1, None, None, 0, 4, 4, 4, None) == native.ERR_INVALID_ARG
     assert L.mvlm_gemv(None, None, 0, None, None, 0, 4, 4, None) == native.ERR_INVALID_ARG
     assert L.mvlm_gemv_q8_0(None, None, None, None, 4, 32, None) == native.ERR_INVALID_ARG

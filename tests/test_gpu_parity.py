@@ -91,6 +91,9 @@ def test_reference_gemms_on_exact_integer_fixtures(dev, orc):
             y = dev.alloc(N * 2)
             dev.gemv(dA, F16, W, y, F16, N, K)
             assert np.array_equal(y.download(np.uint16), C16.ravel())
+            y = dev.alloc(N * 2)
+            dev.gemv_exact(dA, W, y, N, K)
+            assert np.array_equal(y.download(np.uint16), C16.ravel())
 
 
 # ---------------------------------------------------------------------------
@@ -145,6 +148,37 @@ def test_gemv_reference_mode_matches_restated_gemv(dev, orc, N, K):
     assert ok, worst
     # the great majority of outputs round to the very same fp16 as the reference
     assert np.mean(dy.download(np.uint16) == ref16) > 0.95
+
+
+@pytest.mark.parametrize("N,K", [(8192, 2048), (2048, 8192), (6, 300), (37, 1), (4099, 513), (33, 256),
+                                 (130, 1000), (3, 2304), (51200, 64)])
+def test_gemv_exact_bit_exact(dev, orc, N, K):
+    """mvlm_gemv_exact keeps gemv's 256-partial split and fold (gemm.cl:219-270):
+    every fp16 output equals the restated gemv's bit for bit, ragged N and K
+    included (K = 2304 runs 8 windows together and one alone)."""
+    x = orc.normal_f16(K, 141)
+    B = orc.normal_f16(K * N, 142, 0.02)
+    ref16, _ = orc.gemv(x, B, N, K)
+    W = dev.pack(B, F16, N, K, layout=m.LAYOUT_KN)
+    dx, dy = dev.upload(x), dev.alloc(N * 2)
+    dev.gemv_exact(dx, W, dy, N, K)
+    got = dy.download(np.uint16)
+    assert np.array_equal(got, ref16), int(np.sum(got != ref16))
+
+
+def test_gemv_exact_errors(dev, orc):
+    B = orc.normal_f16(32 * 8, 143)
+    W = dev.pack(B, F16, 8, 32, layout=m.LAYOUT_KN)
+    x, y = dev.alloc(64 * 2), dev.alloc(8 * 2)
+    with pytest.raises(m.MvlmError):
+        dev.gemv_exact(x, W, y, 8, 64)          # W is [8 x 32]
+    with pytest.raises(m.MvlmError):
+        dev.gemv_exact(x, W, dev.alloc(4 * 2), 8, 32)   # y holds 4 outputs
+    with pytest.raises(m.MvlmError):
+        dev.gemv_exact(x, dev.pack(B, BF16, 8, 32, layout=m.LAYOUT_KN), y, 8, 32)
+    view = x.view(2, 64)                        # 2-byte offset: x must be 8-byte aligned
+    with pytest.raises(m.MvlmError):
+        dev.gemv_exact(view, W, y, 8, 32)
 
 
 # ---------------------------------------------------------------------------
