@@ -9,6 +9,7 @@
 #include <utility>
 #include <vector>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -131,16 +132,26 @@ inline void launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint3
         hipLaunchKernelGGL(kernel, grid, block, shmem, s, std::forward<Args>(args)...);
 }
 
-// An op made of two dependent kernels: the first carries the start event and
-// Raises kernel Kernel's dynamic LDS limit to `bytes`, once per process (a
-// thread-safe function-local static per kernel); returns that call's status.
+// Raises kernel Kernel's dynamic LDS limit to `bytes` on the current device,
+// once per device and kernel; returns that call's status.  Concurrent first
+// calls may both set the attribute, which is harmless.
 template <auto Kernel>
 inline hipError_t allow_dynamic_lds(int bytes) {
-    static const hipError_t status =
-        hipFuncSetAttribute((const void*)Kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-    return status;
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> status[kMaxDevices];   // 0: not set yet, else hipError_t + 1
+    int dev = 0;
+    if (const hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+    auto set = [&] { return hipFuncSetAttribute((const void*)Kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes); };
+    if (dev < 0 || dev >= kMaxDevices) return set();
+    int st = status[dev].load(std::memory_order_acquire);
+    if (st == 0) {
+        st = (int)set() + 1;
+        status[dev].store(st, std::memory_order_release);
+    }
+    return (hipError_t)(st - 1);
 }
 
+// An op made of two dependent kernels: the first carries the start event and
 // the second the stop event, so plan profiling times the pair.
 enum class LaunchPart { First, Last };
 template <typename... KArgs, typename... Args>

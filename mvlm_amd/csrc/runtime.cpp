@@ -17,12 +17,11 @@ KernelTiming& kernel_timing() {
 }
 
 static bool quiet() {
-    static int q = -1;
-    if (q < 0) {
+    static const bool q = [] {   // read once, thread-safe initialisation
         const char* e = std::getenv("MVLM_QUIET");
-        q = (e && *e && *e != '0') ? 1 : 0;
-    }
-    return q == 1;
+        return e && *e && *e != '0';
+    }();
+    return q;
 }
 
 int set_error(int code, const char* fmt, ...) {
