@@ -93,11 +93,27 @@ __device__ __forceinline__ float apply_epilogue(const E& e, float v, int64_t i, 
     return v;
 }
 
-// Sum over the 64 lanes of a wavefront; every lane receives the total.
+// v + (v of the lane that DPP control `ctrl` names), all lanes valid.
+template <int ctrl>
+__device__ __forceinline__ float add_dpp(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false));
+}
+
+// Sum over the 64 lanes of a wavefront; every lane receives the total.  Four
+// DPP steps (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror) leave each 16-lane row's sum in all its lanes; the four row
+// sums are then read out and added in a fixed order.  No LDS round trips.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+    v = add_dpp<0xB1>(v);
+    v = add_dpp<0x4E>(v);
+    v = add_dpp<0x141>(v);
+    v = add_dpp<0x140>(v);
+    const int b = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return (r0 + r1) + (r2 + r3);
 }
 
 // LDS pointer type of the direct global->LDS loads (global_load_lds_*): lane i
