@@ -229,6 +229,20 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
     }
     __builtin_amdgcn_sched_barrier(0);
 
+    // LDS byte offsets of this lane's x slots.  A valid lane's slice of chunk c
+    // starts at slot (64c + lane) * SL, and x_slot moves its slot v to
+    // v ^ xt with xt = ((lane * SL) >> 4) & (SL - 1) for every c; a lane past K
+    // reads the first slots instead (any in-bounds bytes: its result is
+    // discarded).  So one add per read: xbase[i] + xoff[v].
+    int xbase[CW], xoff[SL];
+#pragma unroll
+    for (int i = 0; i < CW; ++i) xbase[i] = valid[i] ? (64 * (wsub * CW + i) + lane) * SL * 16 : 0;
+    {
+        const int xt = ((lane * SL) >> 4) & (SL - 1);
+#pragma unroll
+        for (int v = 0; v < SL; ++v) xoff[v] = (v ^ xt) << 4;
+    }
+
     // staging done for every wave -> x and scales from LDS, chunk by chunk
     wait_vmcnt<R * CW>();
     __builtin_amdgcn_s_barrier();
@@ -246,7 +260,7 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
             if constexpr (XB >= 16) {
 #pragma unroll
                 for (int v = 0; v < SL; ++v) {
-                    const u32x4 u = reinterpret_cast<const u32x4*>(lds)[x_slot<SL>((xbyte >> 4) + v)];
+                    const u32x4 u = *reinterpret_cast<const u32x4*>(lds + xbase[i] + xoff[v]);
                     xr.d[4 * v + 0] = u[0]; xr.d[4 * v + 1] = u[1];
                     xr.d[4 * v + 2] = u[2]; xr.d[4 * v + 3] = u[3];
                 }
@@ -272,7 +286,7 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
             if constexpr (XB >= 16) {
 #pragma unroll
                 for (int v = 0; v < SL; ++v) {
-                    const u32x4 u = reinterpret_cast<const u32x4*>(xl)[x_slot<SL>((xbyte >> 4) + v)];
+                    const u32x4 u = *reinterpret_cast<const u32x4*>(xl + xbase[i] + xoff[v]);
                     xr.d[4 * v + 0] = u[0]; xr.d[4 * v + 1] = u[1];
                     xr.d[4 * v + 2] = u[2]; xr.d[4 * v + 3] = u[3];
                 }
