@@ -182,10 +182,13 @@ struct StreamGroup {
 // Work shape of one wave by row length in 1 KiB chunks: R rows x CW chunks,
 // the row split over SPLIT waves when it is longer than CW chunks.  A wave
 // keeps 4 to 8 loads of 16 bytes per lane in flight; whole rows per wave
-// (SPLIT = 1) need no combine step.
+// (SPLIT = 1) need no combine step.  The first kByLength shapes are chosen by
+// row length; the last is shape 3 with two rows per wave, used with 2..4 rows
+// of x (each wave then stages half as many x bytes per code byte; with one
+// row of x it measured slower).
 struct Shape { int max_chunks, R, CW, SPLIT; };
-constexpr Shape kShapes[] = {{1, 4, 1, 1}, {2, 2, 2, 1}, {4, 1, 4, 1}, {8, 1, 4, 2}, {16, 1, 8, 2}};
-constexpr int kNumShapes = 5;
+constexpr Shape kShapes[] = {{1, 4, 1, 1}, {2, 2, 2, 1}, {4, 1, 4, 1}, {8, 1, 4, 2}, {16, 1, 8, 2}, {8, 2, 4, 2}};
+constexpr int kNumShapes = 6, kByLength = 5, kBatchLong = 5;
 static_assert(sizeof(kShapes) / sizeof(kShapes[0]) == kNumShapes, "one kernel case per shape");
 
 // The rows [row0, row0 + R) of one wave (those below the block's end rb1),
@@ -404,6 +407,11 @@ __global__ __launch_bounds__(64 * NWAVE, MX == 1 ? F::MIN_WAVES : F::MIN_WAVES_B
         break;
         MVLM_SHAPE_CASE(0) MVLM_SHAPE_CASE(1) MVLM_SHAPE_CASE(2) MVLM_SHAPE_CASE(3) MVLM_SHAPE_CASE(4)
 #undef MVLM_SHAPE_CASE
+    case kBatchLong:
+        if constexpr (MX > 1)
+            stream_rows<F, XT, MX, kShapes[kBatchLong].R, kShapes[kBatchLong].CW, kShapes[kBatchLong].SPLIT>(
+                P, rb0, rb1, s_base, x_stride, x_region, lds, part, wave, lane);
+        break;
     }
 }
 
@@ -413,11 +421,12 @@ static int weight_wpl(int dtype) {
     return dtype == MVLM_Q8_0 ? 16 : dtype == MVLM_Q4_0 ? 32 : 16 / (int)dtype_size(dtype);
 }
 
-// index into kShapes for this weight's row length, -1 if rows are too long
-static int stream_shape(const mvlm_weight* w) {
+// index into kShapes for this weight's row length and mx rows of x, -1 if
+// rows are too long
+static int stream_shape(const mvlm_weight* w, int mx) {
     const int64_t chunks = (weight_row_bytes(w) + 1023) / 1024;
-    for (int i = 0; i < kNumShapes; ++i)
-        if (chunks <= kShapes[i].max_chunks) return i;
+    for (int i = 0; i < kByLength; ++i)
+        if (chunks <= kShapes[i].max_chunks) return (mx > 1 && i == 3) ? kBatchLong : i;
     return -1;
 }
 
@@ -438,7 +447,7 @@ static size_t stream_lds_bytes(const mvlm_weight* w, int x_dtype, int shape, int
 constexpr size_t STREAM_LDS_MAX = 152 * 1024;
 
 bool stream_supported(const mvlm_weight* w, int M) {
-    const int shape = stream_shape(w);
+    const int shape = stream_shape(w, M);
     if (M > 1 && (M > 4 || !is_quant(w->dtype))) return false;
     return shape >= 0 && w->K % weight_wpl(w->dtype) == 0 &&
            stream_lds_bytes(w, MVLM_F32, shape, M > 1 ? 4 : 1) <= STREAM_LDS_MAX;
@@ -507,7 +516,7 @@ hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const*
         p.K = w->K;
         p.y_dtype = y_dtypes[i];
         p.M = M;
-        p.shape = stream_shape(w);
+        p.shape = stream_shape(w, M);
         if (eps && eps[i].any()) {
             p.ep = eps[i];
             p.ep_on = 1;
@@ -551,7 +560,7 @@ hipError_t launch_gemv_stream_batch(hipStream_t s, const float* x, const mvlm_we
     p.K = W->K;
     p.y_dtype = MVLM_F32;
     p.M = M;
-    p.shape = stream_shape(W);
+    p.shape = stream_shape(W, M);
     if (ep && ep->any()) {
         p.ep = *ep;
         p.ep_on = 1;
