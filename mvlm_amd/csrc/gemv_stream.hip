@@ -32,6 +32,8 @@
 #include "common.h"
 #include "device_math.h"
 
+#include <type_traits>
+
 namespace mvlm {
 
 // ---- weight formats --------------------------------------------------------
@@ -95,10 +97,20 @@ __device__ __forceinline__ float chunk_dot(Q8Fmt, u32x4 q, uint16_t dh, const XR
     return __builtin_fmaf(f16_bits_to_f32(dh), s, acc);
 }
 
-// byte j of the block holds weight j (low nibble) and weight j + 16 (high nibble)
+// sum of the 32 x values of one Q4_0 block, in element order
 template <typename XT, int E>
-__device__ __forceinline__ float chunk_dot(Q4Fmt, u32x4 q, uint16_t dh, const XRaw<XT, E>& xr, float acc) {
-    float s = 0.0f, sx = 0.0f;
+__device__ __forceinline__ float x_block_sum(const XRaw<XT, E>& xr) {
+    float sx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) sx += x_at(xr, j);
+    return sx;
+}
+
+// byte j of the block holds weight j (low nibble) and weight j + 16 (high
+// nibble); sx is the block's x_block_sum
+template <typename XT, int E>
+__device__ __forceinline__ float chunk_dot_q4(u32x4 q, uint16_t dh, const XRaw<XT, E>& xr, float sx, float acc) {
+    float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t lo = nibbles_to_bytes(q[i]);
@@ -109,9 +121,12 @@ __device__ __forceinline__ float chunk_dot(Q4Fmt, u32x4 q, uint16_t dh, const XR
             s = __builtin_fmaf(x_at(xr, 16 + 4 * i + e), (float)((hi >> (8 * e)) & 0xFFu), s);
         }
     }
-#pragma unroll
-    for (int j = 0; j < 32; ++j) sx += x_at(xr, j);
     return __builtin_fmaf(f16_bits_to_f32(dh), __builtin_fmaf(-8.0f, sx, s), acc);
+}
+
+template <typename XT, int E>
+__device__ __forceinline__ float chunk_dot(Q4Fmt, u32x4 q, uint16_t dh, const XRaw<XT, E>& xr, float acc) {
+    return chunk_dot_q4(q, dh, xr, x_block_sum(xr), acc);
 }
 
 
@@ -250,6 +265,27 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
     wait_vmcnt<R * CW>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
+    // Q4_0, one row of x: the block sums of x (the -8 offset's term), once per
+    // workgroup into LDS after the scales, instead of once per chunk and wave
+    constexpr bool kSumX = std::is_same_v<F, Q4Fmt> && MX == 1;
+    const float* sxl = reinterpret_cast<const float*>(lds + x_region + ((P.rows_per_block * nb * 2 + 30 + 1023) & ~1023));
+    if constexpr (kSumX) {
+        for (int b = threadIdx.x; b < nb; b += 64 * NWAVE) {
+            XRaw<XT, WPL> xr;
+#pragma unroll
+            for (int v = 0; v < SL; ++v) {
+                const u32x4 u = reinterpret_cast<const u32x4*>(lds)[x_slot<SL>(SL * b + v)];
+                xr.d[4 * v + 0] = u[0]; xr.d[4 * v + 1] = u[1];
+                xr.d[4 * v + 2] = u[2]; xr.d[4 * v + 3] = u[3];
+            }
+            const_cast<float*>(sxl)[b] = x_block_sum(xr);
+        }
+        // LDS-only fences around the barrier: the code loads stay in flight
+        // (a full __syncthreads() would wait for them)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    }
     float acc[R][MX];
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -276,7 +312,9 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
                 uint16_t dh = 0;
                 if constexpr (F::QUANT)
                     dh = *reinterpret_cast<const uint16_t*>(lds + x_region + srow[r] + (kk[i] >> 5) * 2);
-                const float v = chunk_dot(F{}, q[r][i], dh, xr, acc[r][0]);
+                float v;
+                if constexpr (kSumX) v = chunk_dot_q4(q[r][i], dh, xr, sxl[kk[i] >> 5], acc[r][0]);
+                else v = chunk_dot(F{}, q[r][i], dh, xr, acc[r][0]);
                 acc[r][0] = valid[i] ? v : acc[r][0];
             }
             continue;
@@ -441,6 +479,7 @@ static size_t stream_lds_bytes(const mvlm_weight* w, int x_dtype, int shape, int
     size_t bytes = (size_t)mx * ((x_bytes + 1023) & ~(size_t)1023);
     if (is_quant(w->dtype))
         bytes += ((size_t)rows_per_block(shape) * (size_t)(w->K / 32) * 2 + 30 + 1023) & ~(size_t)1023;
+    if (w->dtype == MVLM_Q4_0 && mx == 1) bytes += (size_t)(w->K / 32) * 4;   // block sums of x
     return bytes;
 }
 
