@@ -202,8 +202,9 @@ struct StreamGroup {
 // of x (each wave then stages half as many x bytes per code byte; with one
 // row of x it measured slower).
 struct Shape { int max_chunks, R, CW, SPLIT; };
-constexpr Shape kShapes[] = {{1, 4, 1, 1}, {2, 2, 2, 1}, {4, 1, 4, 1}, {8, 1, 4, 2}, {16, 1, 8, 2}, {8, 2, 4, 2}};
-constexpr int kNumShapes = 6, kByLength = 5, kBatchLong = 5;
+constexpr Shape kShapes[] = {{1, 4, 1, 1}, {2, 2, 2, 1}, {4, 1, 4, 1}, {8, 1, 4, 2}, {16, 1, 8, 2}, {8, 2, 4, 2},
+                             {2, 1, 2, 1}};
+constexpr int kNumShapes = 7, kByLength = 5, kBatchLong = 5, kFewRows2 = 6;
 static_assert(sizeof(kShapes) / sizeof(kShapes[0]) == kNumShapes, "one kernel case per shape");
 
 // The rows [row0, row0 + R) of one wave (those below the block's end rb1),
@@ -445,6 +446,11 @@ __global__ __launch_bounds__(64 * NWAVE, MX == 1 ? F::MIN_WAVES : F::MIN_WAVES_B
         break;
         MVLM_SHAPE_CASE(0) MVLM_SHAPE_CASE(1) MVLM_SHAPE_CASE(2) MVLM_SHAPE_CASE(3) MVLM_SHAPE_CASE(4)
 #undef MVLM_SHAPE_CASE
+    case kFewRows2:
+        if constexpr (MX == 1)
+            stream_rows<F, XT, MX, kShapes[kFewRows2].R, kShapes[kFewRows2].CW, kShapes[kFewRows2].SPLIT>(
+                P, rb0, rb1, s_base, x_stride, x_region, lds, part, wave, lane);
+        break;
     case kBatchLong:
         if constexpr (MX > 1)
             stream_rows<F, XT, MX, kShapes[kBatchLong].R, kShapes[kBatchLong].CW, kShapes[kBatchLong].SPLIT>(
@@ -460,11 +466,16 @@ static int weight_wpl(int dtype) {
 }
 
 // index into kShapes for this weight's row length and mx rows of x, -1 if
-// rows are too long
+// rows are too long.  2-chunk rows with one row of x take one row per wave
+// when two per wave would leave fewer workgroups than MI355X has CUs (256).
 static int stream_shape(const mvlm_weight* w, int mx) {
     const int64_t chunks = (weight_row_bytes(w) + 1023) / 1024;
     for (int i = 0; i < kByLength; ++i)
-        if (chunks <= kShapes[i].max_chunks) return (mx > 1 && i == 3) ? kBatchLong : i;
+        if (chunks <= kShapes[i].max_chunks) {
+            if (mx > 1 && i == 3) return kBatchLong;
+            if (mx == 1 && i == 1 && ((int64_t)w->N + 2 * NWAVE - 1) / (2 * NWAVE) < 256) return kFewRows2;
+            return i;
+        }
     return -1;
 }
 
