@@ -175,7 +175,7 @@ struct Epilogue {
     const void* res = nullptr;
     int act = 0;
     int dtype = 0;
-    bool any() const { return bias || mul || res || act; }
+    __host__ __device__ bool any() const { return bias || mul || res || act; }
 };
 
 // Kernel launchers (defined in the .hip files).  They assume validated input.
@@ -188,10 +188,13 @@ hipError_t launch_gemm_tiled(hipStream_t s, const uint16_t* A, const uint16_t* B
 // summation order (x 8-byte aligned)
 hipError_t launch_gemv_exact(hipStream_t s, const uint16_t* x, const mvlm_weight* W, uint16_t* y);
 hipError_t launch_gemv_dense(hipStream_t s, const void* x, int x_dtype, const mvlm_weight* W,
-                             void* y, int y_dtype, int N, int K);
+                             void* y, int y_dtype, int N, int K, const Epilogue* ep = nullptr);
 // Q8_0 / Q4_0 skinny GEMM on the matrix cores, 1 <= M <= 16 (any row length)
 hipError_t launch_gemm_skinny(hipStream_t s, const float* X, const mvlm_weight* W, float* Y, int M, int N, int K,
                               int num_cus, const Epilogue* ep = nullptr);
+// whether the skinny kernel takes this weight (K a multiple of 32, and every
+// tile shape's LDS, which stages all of a row group's block scales, fits)
+bool skinny_supported(const mvlm_weight* w);
 // M == 1 streaming GEMV for every weight format (rows of at most 16 KiB), and
 // for quantized weights 2 <= M <= 4 rows of x (launch_gemv_stream_batch).
 bool stream_supported(const mvlm_weight* w, int M = 1);

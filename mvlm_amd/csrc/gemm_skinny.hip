@@ -312,6 +312,17 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(const SkinnyGroup 
     }
 }
 
+template <bool Q4>
+static bool skinny_fits(int K) {
+    return skinny_lds_bytes<Q4, 2, 8>(K) <= SKINNY_LDS_MAX && skinny_lds_bytes<Q4, 1, 8>(K) <= SKINNY_LDS_MAX &&
+           skinny_lds_bytes<Q4, 1, 16>(K) <= SKINNY_LDS_MAX;
+}
+
+bool skinny_supported(const mvlm_weight* w) {
+    if (!is_quant(w->dtype) || w->K % 32 != 0) return false;
+    return w->dtype == MVLM_Q4_0 ? skinny_fits<true>(w->K) : skinny_fits<false>(w->K);
+}
+
 template <bool Q4, int R, int NW>
 static hipError_t launch_skinny(hipStream_t s, SkinnyGroup& g) {
     auto kernel = gemm_skinny_kernel<Q4, R, NW>;

@@ -66,7 +66,7 @@ __device__ __forceinline__ void widen_w(u32x4 u, float (&w)[E]) {
 template <typename XT, typename WT, int R>
 __global__ __launch_bounds__(256) void gemv_dense_kernel(const XT* __restrict__ x, const WT* __restrict__ W,
                                                          int64_t ld, void* __restrict__ y, int y_dtype,
-                                                         int N, int K) {
+                                                         int N, int K, const Epilogue ep) {
     constexpr int E = 16 / sizeof(WT);
     const int lane = threadIdx.x & 63;
     const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
@@ -98,7 +98,8 @@ __global__ __launch_bounds__(256) void gemv_dense_kernel(const XT* __restrict__ 
     if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
-            if (row0 + r < N) store_out(y, row0 + r, acc[r], y_dtype);
+            if (row0 + r < N)
+                store_out(y, row0 + r, ep.any() ? apply_epilogue(ep, acc[r], row0 + r, row0 + r) : acc[r], y_dtype);
     }
 }
 
@@ -112,36 +113,37 @@ static int rows_per_wave(int N) {
 
 template <typename XT, typename WT>
 static hipError_t launch_dense_xw(hipStream_t s, const void* x, const mvlm_weight* W, void* y, int y_dtype,
-                                  int N, int K) {
+                                  int N, int K, const Epilogue& ep) {
     int R = rows_per_wave(N);
     unsigned grid = (unsigned)((N + 4 * R - 1) / (4 * R));
     const XT* xp = (const XT*)x;
     const WT* wp = (const WT*)W->data;
     switch (R) {
-        case 4: launch_kernel(gemv_dense_kernel<XT, WT, 4>, dim3(grid), dim3(256), 0, s, xp, wp, W->ld, y, y_dtype, N, K); break;
-        case 2: launch_kernel(gemv_dense_kernel<XT, WT, 2>, dim3(grid), dim3(256), 0, s, xp, wp, W->ld, y, y_dtype, N, K); break;
-        default: launch_kernel(gemv_dense_kernel<XT, WT, 1>, dim3(grid), dim3(256), 0, s, xp, wp, W->ld, y, y_dtype, N, K); break;
+        case 4: launch_kernel(gemv_dense_kernel<XT, WT, 4>, dim3(grid), dim3(256), 0, s, xp, wp, W->ld, y, y_dtype, N, K, ep); break;
+        case 2: launch_kernel(gemv_dense_kernel<XT, WT, 2>, dim3(grid), dim3(256), 0, s, xp, wp, W->ld, y, y_dtype, N, K, ep); break;
+        default: launch_kernel(gemv_dense_kernel<XT, WT, 1>, dim3(grid), dim3(256), 0, s, xp, wp, W->ld, y, y_dtype, N, K, ep); break;
     }
     return hipGetLastError();
 }
 
 template <typename WT>
 static hipError_t launch_dense_w(hipStream_t s, const void* x, int x_dtype, const mvlm_weight* W, void* y,
-                                 int y_dtype, int N, int K) {
+                                 int y_dtype, int N, int K, const Epilogue& ep) {
     switch (x_dtype) {
-        case MVLM_F32: return launch_dense_xw<float, WT>(s, x, W, y, y_dtype, N, K);
-        case MVLM_F16: return launch_dense_xw<__half, WT>(s, x, W, y, y_dtype, N, K);
-        case MVLM_BF16: return launch_dense_xw<__hip_bfloat16, WT>(s, x, W, y, y_dtype, N, K);
+        case MVLM_F32: return launch_dense_xw<float, WT>(s, x, W, y, y_dtype, N, K, ep);
+        case MVLM_F16: return launch_dense_xw<__half, WT>(s, x, W, y, y_dtype, N, K, ep);
+        case MVLM_BF16: return launch_dense_xw<__hip_bfloat16, WT>(s, x, W, y, y_dtype, N, K, ep);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_gemv_dense(hipStream_t s, const void* x, int x_dtype, const mvlm_weight* W, void* y,
-                             int y_dtype, int N, int K) {
+                             int y_dtype, int N, int K, const Epilogue* ep) {
+    const Epilogue e = ep ? *ep : Epilogue{};
     switch (W->dtype) {
-        case MVLM_F32: return launch_dense_w<float>(s, x, x_dtype, W, y, y_dtype, N, K);
-        case MVLM_F16: return launch_dense_w<__half>(s, x, x_dtype, W, y, y_dtype, N, K);
-        case MVLM_BF16: return launch_dense_w<__hip_bfloat16>(s, x, x_dtype, W, y, y_dtype, N, K);
+        case MVLM_F32: return launch_dense_w<float>(s, x, x_dtype, W, y, y_dtype, N, K, e);
+        case MVLM_F16: return launch_dense_w<__half>(s, x, x_dtype, W, y, y_dtype, N, K, e);
+        case MVLM_BF16: return launch_dense_w<__hip_bfloat16>(s, x, x_dtype, W, y, y_dtype, N, K, e);
         default: return hipErrorInvalidValue;
     }
 }

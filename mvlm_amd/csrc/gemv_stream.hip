@@ -467,13 +467,15 @@ static int weight_wpl(int dtype) {
 
 // index into kShapes for this weight's row length and mx rows of x, -1 if
 // rows are too long.  2-chunk rows with one row of x take one row per wave
-// when two per wave would leave fewer workgroups than MI355X has CUs (256).
-static int stream_shape(const mvlm_weight* w, int mx) {
+// when two per wave would leave fewer workgroups than the device has CUs
+// (num_cus > 0; num_cus == 0 keeps the by-length shape, whose LDS footprint
+// bounds the one-row-per-wave variant's).
+static int stream_shape(const mvlm_weight* w, int mx, int num_cus) {
     const int64_t chunks = (weight_row_bytes(w) + 1023) / 1024;
     for (int i = 0; i < kByLength; ++i)
         if (chunks <= kShapes[i].max_chunks) {
             if (mx > 1 && i == 3) return kBatchLong;
-            if (mx == 1 && i == 1 && ((int64_t)w->N + 2 * NWAVE - 1) / (2 * NWAVE) < 256) return kFewRows2;
+            if (mx == 1 && i == 1 && ((int64_t)w->N + 2 * NWAVE - 1) / (2 * NWAVE) < num_cus) return kFewRows2;
             return i;
         }
     return -1;
@@ -497,7 +499,7 @@ static size_t stream_lds_bytes(const mvlm_weight* w, int x_dtype, int shape, int
 constexpr size_t STREAM_LDS_MAX = 152 * 1024;
 
 bool stream_supported(const mvlm_weight* w, int M) {
-    const int shape = stream_shape(w, M);
+    const int shape = stream_shape(w, M, 0);
     if (M > 1 && (M > 4 || !is_quant(w->dtype))) return false;
     return shape >= 0 && w->K % weight_wpl(w->dtype) == 0 &&
            stream_lds_bytes(w, MVLM_F32, shape, M > 1 ? 4 : 1) <= STREAM_LDS_MAX;
@@ -566,7 +568,7 @@ hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const*
         p.K = w->K;
         p.y_dtype = y_dtypes[i];
         p.M = M;
-        p.shape = stream_shape(w, M);
+        p.shape = stream_shape(w, M, num_cus > 0 ? num_cus : 256);
         if (eps && eps[i].any()) {
             p.ep = eps[i];
             p.ep_on = 1;
@@ -576,7 +578,6 @@ hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const*
         lds = b > lds ? b : lds;
     }
     if (lds > STREAM_LDS_MAX) return hipErrorInvalidValue;
-    (void)num_cus;
     if (M > 1) return dtype == MVLM_Q8_0 ? launch_group<Q8Fmt, float, 4>(s, g, lds) : launch_group<Q4Fmt, float, 4>(s, g, lds);
     switch (dtype) {
         case MVLM_Q8_0: return launch_group<Q8Fmt, float>(s, g, lds);
@@ -596,7 +597,6 @@ hipError_t launch_gemv_stream(hipStream_t s, const void* x, int x_dtype, const m
 // Quantized weight, fp32 x [M][K] and y [M][N], 2 <= M <= 4.
 hipError_t launch_gemv_stream_batch(hipStream_t s, const float* x, const mvlm_weight* W, float* y, int M,
                                     int num_cus, const Epilogue* ep) {
-    (void)num_cus;
     if (M < 2 || M > 4 || !stream_supported(W, M)) return hipErrorInvalidValue;
     StreamGroup g{};
     g.count = 1;
@@ -610,7 +610,7 @@ hipError_t launch_gemv_stream_batch(hipStream_t s, const float* x, const mvlm_we
     p.K = W->K;
     p.y_dtype = MVLM_F32;
     p.M = M;
-    p.shape = stream_shape(W, M);
+    p.shape = stream_shape(W, M, num_cus > 0 ? num_cus : 256);
     if (ep && ep->any()) {
         p.ep = *ep;
         p.ep_on = 1;

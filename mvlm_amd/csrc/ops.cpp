@@ -242,6 +242,10 @@ int make_gemv(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, const mvlm_we
         REQUIRE(x_dtype == MVLM_F32 && y_dtype == MVLM_F32, "%s: quantized weights take fp32 x and y", fn);
         NEED(x, (size_t)M * K * 4, "x");
         NEED(y, (size_t)M * N * 4, "y");
+        const bool streams = M == 1 ? stream_supported(W) : (M <= 4 && stream_supported(W, M));
+        if (!streams && !skinny_supported(W))
+            return set_error(MVLM_ERR_UNSUPPORTED, "%s: K=%d is outside the skinny kernel's range (a multiple of 32 "
+                             "whose block scales fit in LDS)", fn, K);
         op->kind = OP_GEMV_QUANT;
         return MVLM_OK;
     }
@@ -278,6 +282,9 @@ int make_gemv_group(mvlm_device* dev, int M, int count, const mvlm_gemv_desc* de
                              (long long)weight_row_bytes(d.W), d.W->K);
         if (M > 1 && d.W->K % 32 != 0)
             return set_error(MVLM_ERR_UNSUPPORTED, "%s: entry %d: K=%d is not a multiple of 32", fn, i, d.W->K);
+        if (M > 1 && !(M <= 4 && stream_supported(d.W, M)) && !skinny_supported(d.W))
+            return set_error(MVLM_ERR_UNSUPPORTED, "%s: entry %d: K=%d is outside the skinny kernel's range", fn, i,
+                             d.W->K);
         op->gx[i] = d.x->ptr;
         op->gw[i] = d.W;
         op->gy[i] = d.y->ptr;
@@ -326,7 +333,7 @@ hipError_t enqueue_op(hipStream_t s, const Op& op) {
         case OP_GEMV_DENSE:
             if (stream_supported(op.w))
                 return launch_gemv_stream(s, op.a, op.a_dtype, op.w, op.c, op.c_dtype, op.num_cus, &op.ep);
-            return launch_gemv_dense(s, op.a, op.a_dtype, op.w, op.c, op.c_dtype, op.N, op.K);
+            return launch_gemv_dense(s, op.a, op.a_dtype, op.w, op.c, op.c_dtype, op.N, op.K, &op.ep);
         case OP_GEMV_QUANT:
             if (op.M == 1 && stream_supported(op.w))
                 return launch_gemv_stream(s, op.a, MVLM_F32, op.w, op.c, MVLM_F32, op.num_cus, &op.ep);

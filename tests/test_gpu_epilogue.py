@@ -135,17 +135,25 @@ def test_quant_gemv_epilogue(dev, orc, qt, N, K, bias, act, mul, residual):
 
 
 @pytest.mark.parametrize("yd", [F32, BF16])
-def test_dense_gemv_epilogue(dev, orc, yd):
-    N, K = 515, 1024
-    x = orc.normal_f16(K, 0x7A)
-    Wt = orc.normal_f16(N * K, 0x7B, 0.05)
-    W = dev.pack(Wt, F16, N, K)
+@pytest.mark.parametrize("wd,N,K", [(F16, 515, 1024), (F16, 70, 300), (F32, 33, 4304)])
+def test_dense_gemv_epilogue(dev, orc, yd, wd, N, K):
+    """Streaming kernel (K=1024) and the per-wave dense kernel that takes rows the
+    streaming kernel does not: F16 with K % 8 != 0, F32 rows over 16 KiB."""
+    if wd == F16:
+        x = orc.normal_f16(K, 0x7A)
+        Wt = orc.normal_f16(N * K, 0x7B, 0.05)
+        x64, W64 = from_storage(orc, x, F16), from_storage(orc, Wt, F16).reshape(N, K)
+    else:
+        x = orc.normal_f32(K, 0x7A)
+        Wt = orc.normal_f32(N * K, 0x7B, 0.05)
+        x64, W64 = x.astype(np.float64), Wt.astype(np.float64).reshape(N, K)
+    W = dev.pack(Wt, wd, N, K)
     ops, vals = make_operands(dev, orc, 1, N, yd, 0x7C, True, True, True)
     y = dev.alloc(N * 4)
-    dev.gemv_ex(dev.upload(x), F16, W, y, yd, N, K, bias=ops["bias"], act=GELU, mul=ops["mul"],
+    dev.gemv_ex(dev.upload(x), wd, W, y, yd, N, K, bias=ops["bias"], act=GELU, mul=ops["mul"],
                 residual=ops["residual"])
     got = from_storage(orc, y.download(np.float32 if yd == F32 else np.uint16, N), yd)[None]
-    Y64, S = orc.gemm_f64(from_storage(orc, x, F16)[None], from_storage(orc, Wt, F16).reshape(N, K), 1, N, K)
+    Y64, S = orc.gemm_f64(x64[None], W64, 1, N, K)
     check(orc, got, Y64, S, vals, GELU, yd, 1e-5)
 
 

@@ -209,8 +209,11 @@ def test_dequant_known_answer_blocks(dev):
         assert np.array_equal(W.dequant().ravel().view(np.uint32), np.array(case["bits"], np.uint32)), case["name"]
 
 
+# (2048, 2048) Q8_0, (2048, 4096) and (300, 3072) Q4_0 have 2 KiB rows with
+# too few rows to give every CU a block at two rows per wave: they take the
+# one-row-per-wave work shape
 QSHAPES = [(6144, 2048), (2048, 8192), (1, 32), (37, 96), (8192, 2048), (3456, 1152), (51200, 2048),
-           (24, 20480), (5, 64)]
+           (24, 20480), (5, 64), (2048, 2048), (2048, 4096), (300, 3072)]
 
 
 @pytest.mark.parametrize("qt", [Q8, Q4])
@@ -451,6 +454,49 @@ def test_gemv_grouped_phi_block(dev, orc, qt):
         _, S = orc.gemm_f64(xs_host[xi].astype(np.float64)[None], deq(b).astype(np.float64).reshape(N, K), 1, N, K)
         ok, worst = within(got, ref, S[0], 1e-5)
         assert ok, (N, K, worst)
+
+
+@pytest.mark.parametrize("qt", [Q8, Q4])
+def test_gemv_grouped_few_rows(dev, orc, qt):
+    """2 KiB rows (Q8_0 K=2048, Q4_0 K=4096) and few rows: one row per wave,
+    grouped with a problem of another work shape"""
+    K2 = 2048 if qt == Q8 else 4096
+    shapes = [(2048, K2), (300, K2 - 1024), (512, 1024)]
+    kind = "q8_0" if qt == Q8 else "q4_0"
+    deq = orc.dequant_q8_0 if qt == Q8 else orc.dequant_q4_0
+    xh = [orc.normal_f32(K, 301 + i) for i, (_, K) in enumerate(shapes)]
+    blocks = [make_quant(orc, qt, N, K, 311 + i) for i, (N, K) in enumerate(shapes)]
+    Ws = [dev.pack(b, qt, N, K) for b, (N, K) in zip(blocks, shapes)]
+    xs = [dev.upload(v) for v in xh]
+    ys = [dev.alloc(N * 4) for N, _ in shapes]
+    dev.gemv_grouped([(x, F32, W, y, F32) for x, W, y in zip(xs, Ws, ys)])
+    for (N, K), x, b, y in zip(shapes, xh, blocks, ys):
+        ref = orc.gemm_nk(kind, x, b, 1, N, K)[0]
+        _, S = orc.gemm_f64(x.astype(np.float64)[None], deq(b).astype(np.float64).reshape(N, K), 1, N, K)
+        ok, worst = within(y.download(np.float32), ref, S[0], 1e-5)
+        assert ok, (N, K, worst)
+
+
+def test_quant_rows_beyond_every_kernel_are_refused(dev):
+    """Q8_0 rows of 65536 weights: too long for the streaming kernel (16 KiB) and
+    their block scales overflow the skinny kernel's LDS: refused when the op is
+    made, before anything is enqueued or captured"""
+    from mvlm_amd import native
+    N, K = 2, 65536
+    W = dev.pack(np.zeros(34 * N * K // 32, np.uint8), Q8, N, K)
+    x, y = dev.alloc(16 * K * 4), dev.alloc(16 * N * 4)
+    for M in (1, 8):
+        with pytest.raises(native.MvlmError) as e:
+            dev.gemm_q8_0(x, W, y, M, N, K)
+        assert e.value.code == native.ERR_UNSUPPORTED, M
+        plan = m.Plan(dev)
+        with pytest.raises(native.MvlmError) as e:
+            plan.add_gemv(x, F32, W, y, F32, M)
+        assert e.value.code == native.ERR_UNSUPPORTED, M
+        plan.destroy()
+    with pytest.raises(native.MvlmError) as e:
+        dev.gemm_quant_grouped(8, [(x, F32, W, y, F32)])
+    assert e.value.code == native.ERR_UNSUPPORTED
 
 
 @pytest.mark.parametrize("qt", [Q8, Q4])
