@@ -153,7 +153,7 @@ inline hipError_t allow_dynamic_lds(int bytes) {
 
 // An op made of two dependent kernels: the first carries the start event and
 // the second the stop event, so plan profiling times the pair.
-enum class LaunchPart { First, Last };
+enum class LaunchPart { First, Middle, Last };
 template <typename... KArgs, typename... Args>
 inline void launch_kernel_part(LaunchPart part, void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t shmem,
                                hipStream_t s, Args&&... args) {
@@ -192,9 +192,10 @@ hipError_t launch_gemv_dense(hipStream_t s, const void* x, int x_dtype, const mv
 // Q8_0 / Q4_0 skinny GEMM on the matrix cores, 1 <= M <= 16 (any row length)
 hipError_t launch_gemm_skinny(hipStream_t s, const float* X, const mvlm_weight* W, float* Y, int M, int N, int K,
                               int num_cus, const Epilogue* ep = nullptr);
-// whether the skinny kernel takes this weight (K a multiple of 32, and every
-// tile shape's LDS, which stages all of a row group's block scales, fits)
-bool skinny_supported(const mvlm_weight* w);
+// whether one skinny launch over these weights fits: K a multiple of 32 and,
+// for the tile shape the launch would pick, the LDS (which stages all of a
+// block's row-group scales) within the limit
+bool skinny_supported(int count, const mvlm_weight* const* ws, int num_cus);
 // M == 1 streaming GEMV for every weight format (rows of at most 16 KiB), and
 // for quantized weights 2 <= M <= 4 rows of x (launch_gemv_stream_batch).
 bool stream_supported(const mvlm_weight* w, int M = 1);
@@ -213,9 +214,13 @@ hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const*
 hipError_t launch_gemm_skinny_group(hipStream_t s, int M, int count, const float* const* Xs,
                                     const mvlm_weight* const* ws, float* const* Ys, int num_cus);
 inline int64_t weight_row_bytes(const mvlm_weight* w) { return is_dense(w->dtype) ? w->ld * (int64_t)dtype_size(w->dtype) : w->ld; }
-// MFMA GEMM; a K split (chosen by the launcher's cost model) needs
-// gemm_workspace_bytes(...) bytes of workspace
-size_t gemm_workspace_bytes(int batch, int M, int N, int K, int num_cus);
+// MFMA GEMM.  Its workspace (gemm_workspace_bytes) holds the fp32 partials
+// of a K split (chosen by the launcher's cost model) and zero-padded copies of
+// A and B when their rows are not 16-byte aligned: K, a leading dimension or
+// a batch stride not a multiple of 8 elements, or B rows readable only up to
+// kread_b < K rounded up to 8.
+size_t gemm_workspace_bytes(int batch, int M, int N, int K, int64_t lda, int64_t ldb, int64_t sA, int64_t sB,
+                            int kread_b, int num_cus);
 hipError_t launch_gemm_mfma(hipStream_t s, const void* A, int ab_dtype, const void* B, void* C,
                             int c_dtype, int batch, int M, int N, int K, int64_t lda, int64_t ldb,
                             int64_t ldc, int64_t strideA, int64_t strideB, int64_t strideC,

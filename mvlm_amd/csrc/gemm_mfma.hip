@@ -421,47 +421,116 @@ static GemmPlan plan_gemm(int M, int N, int K, int batch, int num_cus) {
     return best;
 }
 
-size_t gemm_workspace_bytes(int batch, int M, int N, int K, int num_cus) {
-    const GemmPlan g = plan_gemm(M, N, K, batch, num_cus > 0 ? num_cus : 256);
-    return g.splits > 1 ? (size_t)g.splits * batch * M * N * sizeof(float) : 0;
+// Copies rows of K elements (row r of batch b at src + b*stride + r*ld) into
+// dst [batch][rows][Kp], zero-filling columns K..Kp-1.
+__global__ __launch_bounds__(256) void gemm_pad_rows_kernel(const uint16_t* __restrict__ src, int64_t ld,
+                                                            int64_t stride, int rows, int K, uint16_t* __restrict__ dst,
+                                                            int Kp, int64_t total) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int64_t r = i / Kp;
+        const int k = (int)(i - r * Kp);
+        const int64_t b = r / rows, rr = r - b * rows;
+        dst[i] = k < K ? src[b * stride + rr * ld + k] : (uint16_t)0;
+    }
+}
+
+// Workspace layout: [split partials][padded A][padded B], each 256-byte aligned.
+struct GemmWorkspace {
+    bool pad_a = false, pad_b = false;
+    int kp = 0;                    // K the kernel runs with (zero columns past K)
+    GemmPlan plan{};
+    size_t split_bytes = 0, a_off = 0, b_off = 0, total = 0;
+};
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static GemmWorkspace gemm_workspace(int batch, int M, int N, int K, int64_t lda, int64_t ldb, int64_t sA,
+                                   int64_t sB, int kread_b, int num_cus) {
+    GemmWorkspace w;
+    const int k8 = (int)round_up(K, 8);
+    w.pad_a = K % 8 != 0 || lda % 8 != 0 || (batch > 1 && sA % 8 != 0);
+    w.pad_b = ldb % 8 != 0 || (batch > 1 && sB % 8 != 0) || kread_b < k8;
+    w.kp = (w.pad_a || w.pad_b) ? k8 : K;
+    w.plan = plan_gemm(M, N, w.kp, batch, num_cus > 0 ? num_cus : 256);
+    w.split_bytes = w.plan.splits > 1 ? align256((size_t)w.plan.splits * batch * M * N * sizeof(float)) : 0;
+    w.a_off = w.split_bytes;
+    const size_t a_bytes = w.pad_a ? align256((size_t)batch * M * w.kp * 2) : 0;
+    w.b_off = w.a_off + a_bytes;
+    const size_t b_bytes = w.pad_b ? align256((size_t)batch * N * w.kp * 2) : 0;
+    w.total = w.b_off + b_bytes;
+    return w;
+}
+
+size_t gemm_workspace_bytes(int batch, int M, int N, int K, int64_t lda, int64_t ldb, int64_t sA, int64_t sB,
+                            int kread_b, int num_cus) {
+    return gemm_workspace(batch, M, N, K, lda, ldb, sA, sB, kread_b, num_cus).total;
+}
+
+// Launches kernel `idx` of an op made of `n` kernels (plan profiling times the
+// first kernel's start to the last one's stop).
+template <typename... KArgs, typename... Args>
+static void launch_seq(int idx, int n, void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t s,
+                       Args&&... args) {
+    if (n == 1) launch_kernel(kernel, grid, block, 0, s, std::forward<Args>(args)...);
+    else launch_kernel_part(idx == 0 ? LaunchPart::First : idx == n - 1 ? LaunchPart::Last : LaunchPart::Middle,
+                            kernel, grid, block, 0, s, std::forward<Args>(args)...);
+}
+
+static unsigned pad_grid(int64_t total) {
+    const int64_t b = (total + 255) / 256;
+    return (unsigned)(b < 4096 ? b : 4096);
 }
 
 hipError_t launch_gemm_mfma(hipStream_t s, const void* A, int ab_dtype, const void* B, void* C, int c_dtype,
                             int batch, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
                             int64_t strideA, int64_t strideB, int64_t strideC, int kread_b, int num_cus,
                             const Epilogue* ep, void* workspace, size_t workspace_bytes) {
+    const GemmWorkspace w = gemm_workspace(batch, M, N, K, lda, ldb, strideA, strideB, kread_b, num_cus);
+    if (w.total > 0 && (!workspace || workspace_bytes < w.total)) return hipErrorInvalidValue;
+    const GemmPlan& g = w.plan;
+    const TileCfg& t = *g.tile;
     GemmArgs a{};
     a.A = (const uint16_t*)A; a.B = (const uint16_t*)B; a.C = C; a.c_dtype = c_dtype;
-    a.M = M; a.N = N; a.K = K; a.lda = lda; a.ldb = ldb; a.ldc = ldc;
+    a.M = M; a.N = N; a.K = w.kp; a.lda = lda; a.ldb = ldb; a.ldc = ldc;
     a.sA = strideA; a.sB = strideB; a.sC = strideC;
     a.kread_b = kread_b;
     if (ep && ep->any()) {
         a.ep = *ep;
         a.ep_on = 1;
     }
-    const GemmPlan g = plan_gemm(M, N, K, batch, num_cus > 0 ? num_cus : 256);
-    const TileCfg& t = *g.tile;
     a.tiles_m = (M + t.bm - 1) / t.bm;
     a.tiles_n = (N + t.bn - 1) / t.bn;
     a.splits = g.splits;
     a.split_stages = g.split_stages;
     a.ws = (float*)workspace;
-    if (g.splits > 1 && (!workspace || workspace_bytes < (size_t)g.splits * batch * M * N * sizeof(float)))
-        return hipErrorInvalidValue;
+    const int n = (int)w.pad_a + (int)w.pad_b + 1 + (g.splits > 1 ? 1 : 0);
+    int idx = 0;
+    if (w.pad_a) {
+        uint16_t* ap = (uint16_t*)((char*)workspace + w.a_off);
+        const int64_t total = (int64_t)batch * M * w.kp;
+        launch_seq(idx++, n, gemm_pad_rows_kernel, dim3(pad_grid(total)), dim3(256), s, (const uint16_t*)A, lda,
+                   strideA, M, K, ap, w.kp, total);
+        a.A = ap; a.lda = w.kp; a.sA = (int64_t)M * w.kp;
+    }
+    if (w.pad_b) {
+        uint16_t* bp = (uint16_t*)((char*)workspace + w.b_off);
+        const int64_t total = (int64_t)batch * N * w.kp;
+        launch_seq(idx++, n, gemm_pad_rows_kernel, dim3(pad_grid(total)), dim3(256), s, (const uint16_t*)B, ldb,
+                   strideB, N, min(K, kread_b), bp, w.kp, total);
+        a.B = bp; a.ldb = w.kp; a.sB = (int64_t)N * w.kp; a.kread_b = w.kp;
+    }
     dim3 grid((unsigned)(a.tiles_m * a.tiles_n), 1, (unsigned)(batch * g.splits));
     GemmKernel k = ab_dtype == MVLM_BF16 ? t.bf16 : t.f16;
-    if (g.splits == 1) {
-        launch_kernel(k, grid, dim3(64 * t.waves), 0, s, a);
-        return hipGetLastError();
+    launch_seq(idx++, n, k, grid, dim3(64 * t.waves), s, a);
+    if (g.splits > 1) {
+        const int64_t mn = (int64_t)M * N;
+        if (mn % 4 == 0)
+            launch_seq(idx++, n, gemm_splitk_reduce_kernel<4>, dim3((unsigned)((mn / 4 + 255) / 256), (unsigned)batch),
+                       dim3(256), s, a);
+        else
+            launch_seq(idx++, n, gemm_splitk_reduce_kernel<1>, dim3((unsigned)((mn + 255) / 256), (unsigned)batch),
+                       dim3(256), s, a);
     }
-    launch_kernel_part(LaunchPart::First, k, grid, dim3(64 * t.waves), 0, s, a);
-    const int64_t mn = (int64_t)M * N;
-    if (mn % 4 == 0)
-        launch_kernel_part(LaunchPart::Last, gemm_splitk_reduce_kernel<4>,
-                           dim3((unsigned)((mn / 4 + 255) / 256), (unsigned)batch), dim3(256), 0, s, a);
-    else
-        launch_kernel_part(LaunchPart::Last, gemm_splitk_reduce_kernel<1>,
-                           dim3((unsigned)((mn + 255) / 256), (unsigned)batch), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

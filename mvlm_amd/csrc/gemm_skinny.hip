@@ -312,15 +312,37 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(const SkinnyGroup 
     }
 }
 
-template <bool Q4>
-static bool skinny_fits(int K) {
-    return skinny_lds_bytes<Q4, 2, 8>(K) <= SKINNY_LDS_MAX && skinny_lds_bytes<Q4, 1, 8>(K) <= SKINNY_LDS_MAX &&
-           skinny_lds_bytes<Q4, 1, 16>(K) <= SKINNY_LDS_MAX;
+// Tile shape of a launch by its total 16-row groups: two row groups per
+// block when that still gives every CU a block; fewer row groups than CUs get
+// 16-wave blocks (more loads in flight per block).
+enum SkinnyShape { SK_R2_W8, SK_R1_W8, SK_R1_W16 };
+static SkinnyShape skinny_shape(int64_t groups, int num_cus) {
+    if (groups >= 2 * (int64_t)num_cus) return SK_R2_W8;
+    if (groups >= num_cus) return SK_R1_W8;
+    return SK_R1_W16;
 }
 
-bool skinny_supported(const mvlm_weight* w) {
-    if (!is_quant(w->dtype) || w->K % 32 != 0) return false;
-    return w->dtype == MVLM_Q4_0 ? skinny_fits<true>(w->K) : skinny_fits<false>(w->K);
+template <bool Q4>
+static size_t skinny_lds_for(SkinnyShape sh, int K) {
+    switch (sh) {
+        case SK_R2_W8: return skinny_lds_bytes<Q4, 2, 8>(K);
+        case SK_R1_W8: return skinny_lds_bytes<Q4, 1, 8>(K);
+        default: return skinny_lds_bytes<Q4, 1, 16>(K);
+    }
+}
+
+bool skinny_supported(int count, const mvlm_weight* const* ws, int num_cus) {
+    if (num_cus <= 0) num_cus = 256;
+    int64_t groups = 0;
+    for (int i = 0; i < count; ++i) groups += (ws[i]->N + 15) / 16;
+    const SkinnyShape sh = skinny_shape(groups, num_cus);
+    for (int i = 0; i < count; ++i) {
+        const mvlm_weight* w = ws[i];
+        if (!is_quant(w->dtype) || w->K % 32 != 0) return false;
+        const size_t lds = w->dtype == MVLM_Q4_0 ? skinny_lds_for<true>(sh, w->K) : skinny_lds_for<false>(sh, w->K);
+        if (lds > SKINNY_LDS_MAX) return false;
+    }
+    return true;
 }
 
 template <bool Q4, int R, int NW>
@@ -340,16 +362,16 @@ static hipError_t launch_skinny(hipStream_t s, SkinnyGroup& g) {
     return hipGetLastError();
 }
 
-// Two row groups per block when that still gives every CU a block; fewer
-// row groups than CUs get 16-wave blocks (more loads in flight per block).
 // A grouped launch picks the shape from the row groups of all its problems.
 template <bool Q4>
 static hipError_t launch_skinny_shape(hipStream_t s, SkinnyGroup& g, int num_cus) {
-    int groups = 0;
+    int64_t groups = 0;
     for (int i = 0; i < g.count; ++i) groups += (g.p[i].N + 15) / 16;
-    if (groups >= 2 * num_cus) return launch_skinny<Q4, 2, 8>(s, g);
-    if (groups >= num_cus) return launch_skinny<Q4, 1, 8>(s, g);
-    return launch_skinny<Q4, 1, 16>(s, g);
+    switch (skinny_shape(groups, num_cus)) {
+        case SK_R2_W8: return launch_skinny<Q4, 2, 8>(s, g);
+        case SK_R1_W8: return launch_skinny<Q4, 1, 8>(s, g);
+        default: return launch_skinny<Q4, 1, 16>(s, g);
+    }
 }
 
 static SkinnyProblem skinny_problem(const float* X, const mvlm_weight* W, float* Y) {

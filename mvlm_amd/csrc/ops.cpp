@@ -116,8 +116,10 @@ int make_gemv_exact(mvlm_device* dev, const mvlm_buffer* x, const mvlm_weight* W
     return MVLM_OK;
 }
 
-int make_gemm_packed(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, const mvlm_weight* W, mvlm_buffer* C,
-                     int c_dtype, int M, int N, int K, const char* fn, Op* op) {
+// The op of a packed-weight GEMM, all but its workspace (op->workspace_bytes
+// says how much it needs).
+int make_gemm_packed_op(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, const mvlm_weight* W, mvlm_buffer* C,
+                        int c_dtype, int M, int N, int K, const char* fn, Op* op) {
     REQUIRE(dev && A && W && C, "%s: null argument", fn);
     REQUIRE(A->dev == dev && W->dev == dev && C->dev == dev, "%s: handles belong to another device", fn);
     REQUIRE(M > 0 && N > 0 && K > 0, "%s: M=%d N=%d K=%d must be positive", fn, M, N, K);
@@ -125,7 +127,6 @@ int make_gemm_packed(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, const 
     REQUIRE(W->dtype == MVLM_F16 || W->dtype == MVLM_BF16, "%s: weight dtype %d is not F16/BF16", fn, W->dtype);
     REQUIRE(a_dtype == W->dtype, "%s: activation dtype %d differs from weight dtype %d", fn, a_dtype, W->dtype);
     REQUIRE(is_dense(c_dtype), "%s: output dtype %d is not F32/F16/BF16", fn, c_dtype);
-    if (K % 8 != 0) return set_error(MVLM_ERR_UNSUPPORTED, "%s: K=%d is not a multiple of 8 (16-byte rows)", fn, K);
     REQUIRE(aligned16(A->ptr) && aligned16(C->ptr), "%s: A and C must be 16-byte aligned", fn);
     NEED(A, (size_t)M * K * 2, "A");
     NEED(C, (size_t)M * N * dtype_size(c_dtype), "C");
@@ -136,8 +137,14 @@ int make_gemm_packed(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, const 
     op->lda = K; op->ldb = W->ld; op->ldc = N;
     op->kread_b = (int)W->ld;     // packed rows are zero padded to ld = roundup(K, 64)
     op->num_cus = dev->prop.multiProcessorCount;
-    op->workspace_bytes = gemm_workspace_bytes(1, M, N, K, op->num_cus);
-    return device_scratch(dev, op->workspace_bytes, &op->workspace);
+    op->workspace_bytes = gemm_workspace_bytes(1, M, N, K, op->lda, op->ldb, 0, 0, op->kread_b, op->num_cus);
+    return MVLM_OK;
+}
+
+int make_gemm_packed(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, const mvlm_weight* W, mvlm_buffer* C,
+                     int c_dtype, int M, int N, int K, const char* fn, Op* op) {
+    const int st = make_gemm_packed_op(dev, A, a_dtype, W, C, c_dtype, M, N, K, fn, op);
+    return st != MVLM_OK ? st : device_scratch(dev, op->workspace_bytes, &op->workspace);
 }
 
 int make_gemm_batched(mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer* B, mvlm_buffer* C, int batch,
@@ -148,8 +155,6 @@ int make_gemm_batched(mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer*
     REQUIRE(batch > 0 && M > 0 && N > 0 && K > 0, "%s: batch=%d M=%d N=%d K=%d must be positive", fn, batch, M, N, K);
     REQUIRE(lda >= K && ldb >= K && ldc >= N, "%s: leading dimensions too small", fn);
     REQUIRE(sA >= 0 && sB >= 0 && sC >= 0, "%s: negative batch stride", fn);
-    if (K % 8 != 0 || lda % 8 != 0 || ldb % 8 != 0 || sA % 8 != 0 || sB % 8 != 0)
-        return set_error(MVLM_ERR_UNSUPPORTED, "%s: K, lda, ldb and the A/B strides must be multiples of 8", fn);
     REQUIRE(aligned16(A->ptr) && aligned16(B->ptr) && ((uintptr_t)C->ptr & 3u) == 0,
             "%s: A and B must be 16-byte aligned, C 4-byte aligned", fn);
     NEED(A, ((size_t)(batch - 1) * sA + (size_t)(M - 1) * lda + K) * 2, "A");
@@ -162,7 +167,7 @@ int make_gemm_batched(mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer*
     op->lda = lda; op->ldb = ldb; op->ldc = ldc; op->sA = sA; op->sB = sB; op->sC = sC;
     op->kread_b = K;
     op->num_cus = dev->prop.multiProcessorCount;
-    op->workspace_bytes = gemm_workspace_bytes(batch, M, N, K, op->num_cus);
+    op->workspace_bytes = gemm_workspace_bytes(batch, M, N, K, lda, ldb, sA, sB, K, op->num_cus);
     return device_scratch(dev, op->workspace_bytes, &op->workspace);
 }
 
@@ -243,7 +248,7 @@ int make_gemv(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, const mvlm_we
         NEED(x, (size_t)M * K * 4, "x");
         NEED(y, (size_t)M * N * 4, "y");
         const bool streams = M == 1 ? stream_supported(W) : (M <= 4 && stream_supported(W, M));
-        if (!streams && !skinny_supported(W))
+        if (!streams && !skinny_supported(1, &W, op->num_cus))
             return set_error(MVLM_ERR_UNSUPPORTED, "%s: K=%d is outside the skinny kernel's range (a multiple of 32 "
                              "whose block scales fit in LDS)", fn, K);
         op->kind = OP_GEMV_QUANT;
@@ -282,9 +287,6 @@ int make_gemv_group(mvlm_device* dev, int M, int count, const mvlm_gemv_desc* de
                              (long long)weight_row_bytes(d.W), d.W->K);
         if (M > 1 && d.W->K % 32 != 0)
             return set_error(MVLM_ERR_UNSUPPORTED, "%s: entry %d: K=%d is not a multiple of 32", fn, i, d.W->K);
-        if (M > 1 && !(M <= 4 && stream_supported(d.W, M)) && !skinny_supported(d.W))
-            return set_error(MVLM_ERR_UNSUPPORTED, "%s: entry %d: K=%d is outside the skinny kernel's range", fn, i,
-                             d.W->K);
         op->gx[i] = d.x->ptr;
         op->gw[i] = d.W;
         op->gy[i] = d.y->ptr;
@@ -295,6 +297,12 @@ int make_gemv_group(mvlm_device* dev, int M, int count, const mvlm_gemv_desc* de
     op->M = M;
     op->a_dtype = descs[0].x_dtype;
     op->num_cus = dev->prop.multiProcessorCount;
+    if (M > 1) {   // the skinny kernel serves the group unless every entry streams (launch_group_op)
+        bool stream = M <= 4;
+        for (int i = 0; i < count && stream; ++i) stream = stream_supported(op->gw[i], M);
+        if (!stream && !skinny_supported(count, op->gw, op->num_cus))
+            return set_error(MVLM_ERR_UNSUPPORTED, "%s: the group's block scales exceed the skinny kernel's LDS", fn);
+    }
     return MVLM_OK;
 }
 

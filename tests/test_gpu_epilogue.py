@@ -103,6 +103,22 @@ def test_gemm_packed_epilogue(dev, orc, bias, act, mul, residual, cd):
     check(orc, got, Y64, S, vals, act, cd, 1e-4)
 
 
+def test_patch_embedding_gemm_with_bias(dev, orc):
+    """SigLIP's patch embedding as one GEMM: 729 patches x 588 values (3 x 14 x 14,
+    K not a multiple of 8) against a 1152 x 588 weight, bias in the store, fp16
+    out (moondream2.cpp:774, vision.cl:118-197)"""
+    M, N, K = 729, 1152, 588
+    A = orc.normal_f16(M * K, 0x91)
+    Wt = orc.normal_f16(N * K, 0x92, 0.02)
+    W = dev.pack(Wt, F16, N, K)
+    ops, vals = make_operands(dev, orc, M, N, F16, 0x93, True, False, False)
+    dC = dev.alloc(M * N * 2)
+    dev.gemm_packed_ex(dev.upload(A), F16, W, dC, F16, M, N, K, bias=ops["bias"])
+    got = from_storage(orc, dC.download(np.uint16, M * N), F16).reshape(M, N)
+    Y64, S = orc.gemm_f64(from_storage(orc, A, F16).reshape(M, K), from_storage(orc, Wt, F16).reshape(N, K), M, N, K)
+    check(orc, got, Y64, S, vals, NONE, F16, 1e-3)
+
+
 def test_gemm_epilogue_residual_in_place(dev, orc):
     """residual aliasing the output: C = gelu(A W^T + b) + C"""
     M, N, K = 64, 96, 128

@@ -83,10 +83,9 @@ def test_reference_gemms_on_exact_integer_fixtures(dev, orc):
             assert np.array_equal(dC.download(np.uint16), C16.ravel())
         # the same integers through the packed MFMA path and the GEMV are exact too
         W = dev.pack(B, F16, N, K, layout=m.LAYOUT_KN)
-        if K % 8 == 0:
-            dC = dev.alloc(M * N * 4)
-            dev.gemm_packed(dA, F16, W, dC, F32, M, N, K)
-            assert np.array_equal(dC.download(np.float32), C16.view(np.float16).astype(np.float32).ravel())
+        dC = dev.alloc(M * N * 4)
+        dev.gemm_packed(dA, F16, W, dC, F32, M, N, K)
+        assert np.array_equal(dC.download(np.float32), C16.view(np.float16).astype(np.float32).ravel())
         if M == 1:
             y = dev.alloc(N * 2)
             dev.gemv(dA, F16, W, y, F16, N, K)
@@ -333,6 +332,37 @@ def test_gemm_packed_model_shapes(dev, orc, M, N, K):
     check_packed(dev, orc, M, N, K, F16, F32, rows=24)
 
 
+@pytest.mark.parametrize("M,N,K", [(3, 5, 1), (17, 33, 7), (64, 70, 9), (100, 130, 588), (729, 1152, 588)])
+@pytest.mark.parametrize("ab,cd", [(F16, F32), (BF16, BF16)])
+def test_gemm_packed_any_k(dev, orc, M, N, K, ab, cd):
+    """K not a multiple of 8 (gemm_image takes any K, gemm.cl:157-200): A's rows are
+    not 16-byte aligned, so they are copied zero-padded into the workspace first;
+    729x1152x588 is SigLIP's patch embedding (3x14x14 patch values per token)"""
+    check_packed(dev, orc, M, N, K, ab, cd, rows=None if M < 200 else 40)
+
+
+@pytest.mark.parametrize("batch,M,N,K,lda,ldb,sA,sB", [(3, 33, 40, 13, 15, 17, 33 * 15 + 1, 40 * 17 + 3),
+                                                       (2, 65, 64, 72, 77, 72, 65 * 77, 64 * 72),
+                                                       (4, 16, 24, 5, 5, 5, 80, 120)])
+def test_gemm_batched_unaligned_rows(dev, orc, batch, M, N, K, lda, ldb, sA, sB):
+    """batched NT products whose K, leading dimensions or batch strides leave rows
+    off the 16-byte grid (both operands padded into the workspace)"""
+    nA = (batch - 1) * sA + (M - 1) * lda + K
+    nB = (batch - 1) * sB + (N - 1) * ldb + K
+    A = orc.normal_f16(nA, 401)
+    B = orc.normal_f16(nB, 402)
+    dC = dev.alloc(batch * M * N * 4)
+    dev.gemm_batched(dev.upload(A), dev.upload(B), dC, batch, M, N, K, lda, ldb, N, sA, sB, M * N)
+    got = dC.download(np.float32).reshape(batch, M, N)
+    for b in range(batch):
+        a = np.stack([A[b * sA + r * lda: b * sA + r * lda + K] for r in range(M)])
+        w = np.stack([B[b * sB + r * ldb: b * sB + r * ldb + K] for r in range(N)])
+        ref = orc.gemm_nk("f16", a.copy(), w.copy(), M, N, K)
+        _, Sc = orc.gemm_f64(orc.f16_to_f32(a).astype(np.float64), orc.f16_to_f32(w).astype(np.float64), M, N, K)
+        ok, worst = within(got[b], ref, Sc, 1e-3)
+        assert ok, (b, worst)
+
+
 def test_gemm_packed_kn_layout_equals_nk(dev, orc):
     check_packed(dev, orc, 50, 72, 96, F16, F32, layout=m.LAYOUT_KN)
 
@@ -405,8 +435,8 @@ def test_errors_with_live_device(dev):
     assert e.value.code == native.ERR_INVALID_ARG
     Wf = dev.pack(np.zeros(3 * 12, np.uint16), F16, 3, 12)
     with pytest.raises(native.MvlmError) as e:
-        dev.gemm_packed(dev.alloc(12 * 2 * 2), F16, Wf, dev.alloc(64), F32, 2, 3, 12)   # K % 8
-    assert e.value.code == native.ERR_UNSUPPORTED
+        dev.gemm_packed(dev.alloc(12 * 2 * 2 - 2), F16, Wf, dev.alloc(64), F32, 2, 3, 12)   # A one element short
+    assert e.value.code == native.ERR_BUFFER_TOO_SMALL
 
 
 def test_event_timing(dev, orc):
@@ -478,11 +508,11 @@ def test_gemv_grouped_few_rows(dev, orc, qt):
 
 
 def test_quant_rows_beyond_every_kernel_are_refused(dev):
-    """Q8_0 rows of 65536 weights: too long for the streaming kernel (16 KiB) and
+    """Q8_0 rows of 131072 weights: too long for the streaming kernel (16 KiB) and
     their block scales overflow the skinny kernel's LDS: refused when the op is
     made, before anything is enqueued or captured"""
     from mvlm_amd import native
-    N, K = 2, 65536
+    N, K = 2, 131072
     W = dev.pack(np.zeros(34 * N * K // 32, np.uint8), Q8, N, K)
     x, y = dev.alloc(16 * K * 4), dev.alloc(16 * N * 4)
     for M in (1, 8):
