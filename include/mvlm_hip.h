@@ -193,6 +193,20 @@ int mvlm_gemm_packed_ex(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, con
 int mvlm_gemv_ex(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W,
                  mvlm_buffer* y, int y_dtype, int N, int K, const mvlm_epilogue* ep, mvlm_event** ev);
 
+/* mvlm_gemm_packed_ex without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * workspace (K-split partials, zero-padded copies of A when K % 8 != 0) comes
+ * from one fixed device array of MVLM_NOALLOC_SCRATCH_BYTES per GPU, reserved
+ * by the library for the life of the process; a shape that needs more is
+ * refused with MVLM_ERR_UNSUPPORTED.  Results are identical to
+ * mvlm_gemm_packed_ex's.  All calls on one GPU share the array: calls through
+ * one device handle run in order on its stream, calls that overlap on one GPU
+ * (several handles or streams) race.  No event is returned. */
+#define MVLM_NOALLOC_SCRATCH_BYTES (32u << 20)
+int mvlm_gemm_packed_ex_noalloc(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, const mvlm_weight* W,
+                                mvlm_buffer* C, int c_dtype, int M, int N, int K, const mvlm_epilogue* ep);
+
 /* ---- grouped decode GEMV ----------------------------------------------------
  * Up to MVLM_MAX_GROUP independent GEMVs (M = 1) in one launch, e.g. the
  * projections of one Phi-1.5 block that do not depend on each other: QKV and

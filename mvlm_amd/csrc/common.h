@@ -28,6 +28,10 @@ struct mvlm_device {
     // order, so they share the current block.
     std::vector<void*> scratch_blocks;
     size_t scratch_bytes = 0;
+    // Device address of the library's fixed workspace array on this GPU
+    // (MVLM_NOALLOC_SCRATCH_BYTES, noalloc.hip), used only by the entry points
+    // that allocate nothing; resolved at device creation.
+    void* noalloc_scratch = nullptr;
 };
 
 struct mvlm_buffer {
@@ -100,6 +104,9 @@ inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
 // Device workspace of at least `bytes` (see mvlm_device::scratch_blocks).
 int device_scratch(mvlm_device* dev, size_t bytes, void** out);
+// Looks up the fixed workspace array's address on the current device
+// (noalloc.hip); sets dev->noalloc_scratch.
+int resolve_noalloc_scratch(mvlm_device* dev);
 
 // Launch bracketing: records the start marker when the caller asked for an
 // event, and finishes (end marker + hand-over) after the launch.

@@ -419,6 +419,25 @@ extern "C" int mvlm_gemm_packed_ex(mvlm_device* dev, const mvlm_buffer* A, int a
              [&] { return make_epilogue(dev, ep, M, N, c_dtype, fn, &op.ep); }));
 }
 
+extern "C" int mvlm_gemm_packed_ex_noalloc(mvlm_device* dev, const mvlm_buffer* A, int a_dtype, const mvlm_weight* W,
+                                           mvlm_buffer* C, int c_dtype, int M, int N, int K,
+                                           const mvlm_epilogue* ep) {
+    const char* fn = __func__;
+    Op op{};
+    int st = make_gemm_packed_op(dev, A, a_dtype, W, C, c_dtype, M, N, K, fn, &op);
+    if (st == MVLM_OK) st = make_epilogue(dev, ep, M, N, c_dtype, fn, &op.ep);
+    if (st != MVLM_OK) return st;
+    if (op.workspace_bytes > (size_t)MVLM_NOALLOC_SCRATCH_BYTES)
+        return set_error(MVLM_ERR_UNSUPPORTED, "%s: %dx%dx%d needs %zu bytes of workspace, above the %zu bytes this "
+                         "entry point holds; use mvlm_gemm_packed_ex", fn, M, N, K, op.workspace_bytes,
+                         (size_t)MVLM_NOALLOC_SCRATCH_BYTES);
+    if (op.workspace_bytes > 0) {
+        if (!dev->noalloc_scratch) return set_error(MVLM_ERR_HIP, "%s: the fixed workspace was not resolved", fn);
+        op.workspace = dev->noalloc_scratch;
+    }
+    return run_one(dev, op, nullptr, fn);
+}
+
 extern "C" int mvlm_gemm_batched(mvlm_device* dev, const mvlm_buffer* A, const mvlm_buffer* B, mvlm_buffer* C,
                                  int batch, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
                                  int64_t strideA, int64_t strideB, int64_t strideC, mvlm_event** ev) {

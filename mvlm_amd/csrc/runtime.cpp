@@ -113,6 +113,7 @@ extern "C" int mvlm_device_create(int ordinal, mvlm_device** out) {
     d->ordinal = ordinal;
     int st = check_hip(hipGetDeviceProperties(&d->prop, ordinal), "hipGetDeviceProperties");
     if (st == MVLM_OK) st = check_hip(hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking), "hipStreamCreate");
+    if (st == MVLM_OK) st = resolve_noalloc_scratch(d);
     if (st != MVLM_OK) {
         if (d->stream) (void)hipStreamDestroy(d->stream);
         delete d;

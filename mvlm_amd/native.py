@@ -104,6 +104,7 @@ _SIGNATURES = {
     "mvlm_gemv_grouped": (c_int, [_P, c_int, POINTER(GemvDesc), _PP]),
     "mvlm_gemm_packed_ex": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, c_int, c_int, POINTER(Epilogue), _PP]),
     "mvlm_gemv_ex": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, c_int, POINTER(Epilogue), _PP]),
+    "mvlm_gemm_packed_ex_noalloc": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, c_int, c_int, POINTER(Epilogue)]),
     "mvlm_plan_add_gemv_ex": (c_int, [_P, _P, c_int, _P, _P, c_int, POINTER(Epilogue)]),
     "mvlm_plan_add_gemm_packed_ex": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, POINTER(Epilogue)]),
     "mvlm_plan_add_gemv_grouped": (c_int, [_P, c_int, POINTER(GemvDesc)]),
@@ -564,6 +565,13 @@ class Device:
         ep = _epilogue(bias, act, mul, residual)
         return self._launch("mvlm_gemm_packed_ex", (A.handle, a_dtype, W.handle, C.handle, c_dtype, M, N, K,
                                                      byref(ep)), event)
+
+    def gemm_packed_ex_noalloc(self, A, a_dtype, W, C, c_dtype, M, N, K, bias=None, act=ACT_NONE, mul=None,
+                               residual=None):
+        """mvlm_gemm_packed_ex with its workspace in the library's fixed per-GPU array (no allocation)."""
+        ep = _epilogue(bias, act, mul, residual)
+        _call("mvlm_gemm_packed_ex_noalloc", self.handle, A.handle, a_dtype, W.handle, C.handle, c_dtype, M, N, K,
+              byref(ep))
 
     def gemv_ex(self, x, x_dtype, W, y, y_dtype, N, K, bias=None, act=ACT_NONE, mul=None, residual=None,
                 event=False):
