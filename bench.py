@@ -406,6 +406,82 @@ def pmc_probe(steps=3):
     print("pmc probe done", flush=True)
 
 
+PMC_WORKLOADS = ("decode_q8_0_m1", "decode_q4_0_m1", "decode_q4_0_m4", "decode_q4_0_m16", "decode_q8_0_m4", "gemm")
+
+
+def pmc_workload(name, reps=2):
+    """Workload of a counter run (rocprofv3 --pmc): `reps` eager passes of one
+    decode step (decode_<qt>_m<M>, grouped like the bench) or of every GEMM
+    shape of --gemm-only (one launch plan each), then the calibration copy of
+    pmc_probe.  Prints one line per pass."""
+    import mvlm_amd as m
+    import torch
+    dev = m.Device(0)
+    plans, weights = [], []
+    if name.startswith("decode_"):
+        _, qt0, qt1, mm = name.split("_")
+        plan, ws, _ = build_decode_plan(dev, m, f"{qt0}_{qt1}", int(mm[1:]), True)
+        plans.append((name, plan))
+        weights += ws
+    elif name == "gemm":
+        for wname, M, N, K in GEMM_SHAPES:
+            W = dev.random_weight(m.F16, N, K, SEED ^ (zlib.crc32(wname.encode()) & 0xFFFF), 0.02)
+            A = dev.fill_normal(dev.alloc(M * K * 2), m.F16, M * K, SEED ^ 0x300, 1.0)
+            C = dev.alloc(M * N * 4)
+            plan = m.Plan(dev)
+            plan.add_gemm_packed(A, m.F16, W, C, m.F32, M)
+            plans.append((wname, plan))
+            weights.append(W)
+    else:
+        raise SystemExit(f"unknown counter workload {name}; one of {', '.join(PMC_WORKLOADS)}")
+    for r in range(reps):
+        for pname, plan in plans:
+            plan.run(1)
+            dev.sync()
+        print(f"pmc {name} pass {r} done", flush=True)
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    for _, plan in plans:
+        plan.destroy()
+    for W in weights:
+        W.free()
+    dev.close()
+    print("pmc probe done", flush=True)
+
+
+def counter_table(dirs, kernel_filter=""):
+    """Per (kernel, grid) mean per dispatch of every counter found in the
+    counter_collection.csv files under `dirs`, as a markdown table (stdout)."""
+    import csv
+    import glob
+    per = {}
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            seen = {}
+            for r in csv.DictReader(open(f)):
+                name = r["Kernel_Name"]
+                if kernel_filter not in name:
+                    continue
+                key = (name, r.get("Grid_Size", ""))
+                disp = (f, int(r["Dispatch_Id"]))
+                e = per.setdefault(key, {})
+                c = e.setdefault(r["Counter_Name"], {})
+                c[disp] = c.get(disp, 0.0) + float(r["Counter_Value"])
+                seen[disp] = 1
+    counters = sorted({c for e in per.values() for c in e})
+    print("| kernel | grid | dispatches | " + " | ".join(counters) + " |")
+    print("|---|---|---|" + "---|" * len(counters))
+    for (name, grid), e in sorted(per.items()):
+        n = max(len(v) for v in e.values())
+        cells = [f"{np.mean(list(e[c].values())):.4g}" if c in e else "" for c in counters]
+        short = name.split("(")[0].replace("void ", "")[:70]
+        print(f"| `{short}` | {grid} | {n} | " + " | ".join(cells) + " |")
+
+
 def _counter_rows(d):
     import csv
     import glob
@@ -468,6 +544,11 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true", help="enqueue plans eagerly instead of replaying HIP graphs")
     ap.add_argument("--pmc-probe", action="store_true", help="workload for rocprofv3 --pmc traffic runs")
+    ap.add_argument("--pmc-workload", choices=PMC_WORKLOADS,
+                    help="workload for rocprofv3 --pmc counter runs (eager passes, see pmc_workload)")
+    ap.add_argument("--counter-table", nargs="+", metavar="DIR",
+                    help="markdown table of the counters collected under DIR(s) (per kernel and grid)")
+    ap.add_argument("--kernel-filter", default="", help="with --counter-table: kernels whose name contains this")
     ap.add_argument("--attention-only", action="store_true",
                     help="only the attention and token-pick workloads (one JSON line of them)")
     ap.add_argument("--gemm-only", action="store_true",
@@ -480,6 +561,12 @@ def main():
         return
     if args.pmc_probe:
         pmc_probe()
+        return
+    if args.pmc_workload:
+        pmc_workload(args.pmc_workload)
+        return
+    if args.counter_table:
+        counter_table(args.counter_table, args.kernel_filter)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this library has no multi-GPU path (the decode GEMV would shard "
