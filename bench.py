@@ -75,31 +75,40 @@ def profile_plan(plan, reps=5):
 # workloads
 # ---------------------------------------------------------------------------
 
+def decode_inputs(dev, m, M):
+    """The three activation inputs of a decode step: the block input (QKV, fc1 and
+    the LM head read it), the attention output (dense) and the MLP hidden (fc2)."""
+    ln = dev.fill_normal(dev.alloc(M * 2048 * 4), m.F32, M * 2048, SEED ^ 0x11, 1.0)
+    attn = dev.fill_normal(dev.alloc(M * 2048 * 4), m.F32, M * 2048, SEED ^ 0x12, 1.0)
+    gelu = dev.fill_normal(dev.alloc(M * 8192 * 4), m.F32, M * 8192, SEED ^ 0x13, 1.0)
+    return {"qkv": ln, "fc1": ln, "dense": attn, "fc2": gelu, "lm_head": ln}
+
+
 def build_decode_plan(dev, m, qt, M, grouped=True):
     """The plan of one Phi-1.5 decode step over quantized weights, M rows of
-    activations (see decode_step).  Returns (plan, weights, grouped)."""
+    activations (see decode_step); every GEMV writes its own output buffer.
+    Returns (plan, weights, grouped, io) with io = {"x": GEMV name -> input,
+    "y": outputs in PHI_STEP order}."""
     qdt = m.Q8_0 if qt == "q8_0" else m.Q4_0
     weights = [dev.random_weight(qdt, N, K, SEED ^ (0x100 + i), 0.02) for i, (_, N, K) in enumerate(PHI_STEP)]
-    ln = dev.fill_normal(dev.alloc(M * 2048 * 4), m.F32, M * 2048, SEED ^ 0x11, 1.0)     # block input
-    attn = dev.fill_normal(dev.alloc(M * 2048 * 4), m.F32, M * 2048, SEED ^ 0x12, 1.0)   # attention out
-    gelu = dev.fill_normal(dev.alloc(M * 8192 * 4), m.F32, M * 8192, SEED ^ 0x13, 1.0)   # MLP hidden
-    x_of = {"qkv": ln, "fc1": ln, "dense": attn, "fc2": gelu, "lm_head": ln}
-    ys = {name: dev.alloc(M * N * 4) for name, N, _ in PHI_LAYER + [PHI_LM_HEAD]}
+    x_of = decode_inputs(dev, m, M)
+    ys = [dev.alloc(M * N * 4) for _, N, _ in PHI_STEP]
     plan = m.Plan(dev)
     if grouped:
         for layer in range(24):
-            w = dict(zip(("qkv", "dense", "fc1", "fc2"), weights[4 * layer: 4 * layer + 4]))
+            i0 = 4 * layer
+            idx = dict(zip(("qkv", "dense", "fc1", "fc2"), range(i0, i0 + 4)))
             for pair in (("qkv", "fc1"), ("dense", "fc2")):
-                entries = [(x_of[n], m.F32, w[n], ys[n], m.F32) for n in pair]
+                entries = [(x_of[n], m.F32, weights[idx[n]], ys[idx[n]], m.F32) for n in pair]
                 if M == 1:
                     plan.add_gemv_grouped(entries)
                 else:
                     plan.add_gemm_quant_grouped(M, entries)
-        plan.add_gemv(ln, m.F32, weights[-1], ys["lm_head"], m.F32, M)
+        plan.add_gemv(x_of["lm_head"], m.F32, weights[-1], ys[-1], m.F32, M)
     else:
-        for W, (name, N, K) in zip(weights, PHI_STEP):
-            plan.add_gemv(x_of[name], m.F32, W, ys[name], m.F32, M)
-    return plan, weights, grouped
+        for W, y, (name, N, K) in zip(weights, ys, PHI_STEP):
+            plan.add_gemv(x_of[name], m.F32, W, y, m.F32, M)
+    return plan, weights, grouped, {"x": x_of, "y": ys}
 
 
 def decode_step(dev, m, qt, M, steps, warmup, graph=True, grouped=True):
@@ -110,7 +119,7 @@ def decode_step(dev, m, qt, M, steps, warmup, graph=True, grouped=True):
     dense (on the attention output) and fc2 (on the GELU output).  grouped=True
     issues each independent pair as one grouped launch (2 launches per layer +
     the LM head = 49); grouped=False issues the 97 GEMVs one launch each."""
-    plan, weights, grouped = build_decode_plan(dev, m, qt, M, grouped)
+    plan, weights, grouped, _ = build_decode_plan(dev, m, qt, M, grouped)
     per_op = profile_plan(plan)
     if graph:
         plan.use_graph(True)
@@ -139,18 +148,28 @@ def decode_step(dev, m, qt, M, steps, warmup, graph=True, grouped=True):
     return res
 
 
-def decode_token(dev, m, qt, cache, steps, warmup):
-    """One Phi-1.5 decode step with the path's own ops end to end: per layer the
-    grouped {QKV, fc1} GEMV, attention of the new token against a `cache`-entry
-    fp16 KV cache (32 heads of 64), the grouped {dense, fc2} GEMV; then the LM
-    head and the on-device token pick.  Layer norm, rotary embedding, the KV
-    append and GELU are not part of this path and are left out."""
+def build_token_plan(dev, m, qt, cache):
+    """The plan of one Phi-1.5 decode step with the path's own ops end to end: per
+    layer the grouped {QKV, fc1} GEMV, attention of the new token against a
+    `cache`-entry fp16 KV cache (32 heads of 64), the grouped {dense, fc2} GEMV;
+    then the LM head and the on-device token pick.  Layer norm, rotary
+    embedding, the KV append and GELU are not part of this path and are left
+    out.  The grouped launches carry the epilogues of the block's projections:
+    QKV + bias, fc1 + bias + GELU, dense + bias + residual, fc2 + bias +
+    residual (the residual stream h; each branch writes its own output).
+    Returns (plan, weights, io) with io = {"x", "y" (PHI_STEP order), "ep"
+    (per GEMV: dict of bias / act / residual buffers, or None), "token", "q",
+    "k", "v", "o"}."""
     qdt = m.Q8_0 if qt == "q8_0" else m.Q4_0
     weights = [dev.random_weight(qdt, N, K, SEED ^ (0x100 + i), 0.02) for i, (_, N, K) in enumerate(PHI_STEP)]
-    ln = dev.fill_normal(dev.alloc(2048 * 4), m.F32, 2048, SEED ^ 0x11, 1.0)
-    att = dev.fill_normal(dev.alloc(2048 * 4), m.F32, 2048, SEED ^ 0x12, 1.0)
-    gelu = dev.fill_normal(dev.alloc(8192 * 4), m.F32, 8192, SEED ^ 0x13, 1.0)
-    ys = {name: dev.alloc(N * 4) for name, N, _ in PHI_LAYER + [PHI_LM_HEAD]}
+    x_of = decode_inputs(dev, m, 1)
+    ys = [dev.alloc(N * 4) for _, N, _ in PHI_STEP]
+    h = dev.fill_normal(dev.alloc(2048 * 4), m.F32, 2048, SEED ^ 0x14, 1.0)        # residual stream
+    bias = {name: dev.fill_normal(dev.alloc(N * 4), m.F32, N, SEED ^ (0x20 + j), 0.02)
+            for j, (name, N, _) in enumerate(PHI_LAYER)}
+    ep_of = {"qkv": {"bias": bias["qkv"]}, "fc1": {"bias": bias["fc1"], "act": m.native.ACT_GELU_TANH},
+             "dense": {"bias": bias["dense"], "residual": h}, "fc2": {"bias": bias["fc2"], "residual": h}}
+    eps = [ep_of.get(name) for name, _, _ in PHI_STEP]
     H, D = 32, 64
     q = dev.fill_normal(dev.alloc(H * D * 2), m.F16, H * D, SEED ^ 0x701, 1.0)
     k = dev.fill_normal(dev.alloc(cache * H * D * 2), m.F16, cache * H * D, SEED ^ 0x702, 1.0)
@@ -159,20 +178,30 @@ def decode_token(dev, m, qt, cache, steps, warmup):
     tok = dev.alloc(4)
     plan = m.Plan(dev)
     for layer in range(24):
-        w = dict(zip(("qkv", "dense", "fc1", "fc2"), weights[4 * layer: 4 * layer + 4]))
-        plan.add_gemv_grouped([(ln, m.F32, w["qkv"], ys["qkv"], m.F32), (ln, m.F32, w["fc1"], ys["fc1"], m.F32)])
+        i0 = 4 * layer
+        plan.add_gemv_grouped([(x_of["qkv"], m.F32, weights[i0], ys[i0], m.F32),
+                               (x_of["fc1"], m.F32, weights[i0 + 2], ys[i0 + 2], m.F32)],
+                              epilogues=[eps[i0], eps[i0 + 2]])
         plan.add_attention(q, k, v, o, m.F16, 1, cache, H, D, causal=False)
-        plan.add_gemv_grouped([(att, m.F32, w["dense"], ys["dense"], m.F32),
-                               (gelu, m.F32, w["fc2"], ys["fc2"], m.F32)])
-    plan.add_gemv(ln, m.F32, weights[-1], ys["lm_head"], m.F32, 1)
-    plan.add_argmax(ys["lm_head"], m.F32, 1, 51200, 51200, tok)
+        plan.add_gemv_grouped([(x_of["dense"], m.F32, weights[i0 + 1], ys[i0 + 1], m.F32),
+                               (x_of["fc2"], m.F32, weights[i0 + 3], ys[i0 + 3], m.F32)],
+                              epilogues=[eps[i0 + 1], eps[i0 + 3]])
+    plan.add_gemv(x_of["lm_head"], m.F32, weights[-1], ys[-1], m.F32, 1)
+    plan.add_argmax(ys[-1], m.F32, 1, 51200, 51200, tok)
+    return plan, weights, {"x": x_of, "y": ys, "ep": eps, "token": tok, "q": q, "k": k, "v": v, "o": o}
+
+
+def decode_token(dev, m, qt, cache, steps, warmup):
+    """One Phi-1.5 decode step with the path's own ops end to end (build_token_plan)."""
+    plan, weights, _ = build_token_plan(dev, m, qt, cache)
     plan.use_graph(True)
     ms = timed_plan(dev, plan, steps, warmup)
     plan.destroy()
     for W in weights:
         W.free()
     return {"workload": f"phi15_decode_token_{qt}_cache{cache}", "us": ms * 1e3, "tokens_per_s": 1e3 / ms,
-            "ops": 24 * 3 + 2}
+            "ops": 24 * 3 + 2, "epilogues": "QKV+bias, fc1+bias+GELU, dense+bias+residual, fc2+bias+residual "
+                                            "fused into the grouped GEMVs"}
 
 
 def fp32_gemv(dev, m, steps, warmup, copies=16):
@@ -388,7 +417,7 @@ def pmc_probe(steps=3):
     import mvlm_amd as m
     import torch
     dev = m.Device(0)
-    plan, weights, _ = build_decode_plan(dev, m, "q8_0", 1, True)
+    plan, weights, _, _ = build_decode_plan(dev, m, "q8_0", 1, True)
     plan.run(1)
     dev.sync()
     plan.run(steps)
@@ -420,7 +449,7 @@ def pmc_workload(name, reps=2):
     plans, weights = [], []
     if name.startswith("decode_"):
         _, qt0, qt1, mm = name.split("_")
-        plan, ws, _ = build_decode_plan(dev, m, f"{qt0}_{qt1}", int(mm[1:]), True)
+        plan, ws, _, _ = build_decode_plan(dev, m, f"{qt0}_{qt1}", int(mm[1:]), True)
         plans.append((name, plan))
         weights += ws
     elif name == "gemm":

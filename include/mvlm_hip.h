@@ -228,6 +228,15 @@ int mvlm_gemv_grouped(mvlm_device* dev, int count, const mvlm_gemv_desc* descs, 
  * Y[M,N] = X[M,K] * W^T with fp32 X and Y and the checks of mvlm_gemm_q8_0 /
  * mvlm_gemm_q4_0, 1 <= M <= 16, one weight dtype for all entries. */
 int mvlm_gemm_quant_grouped(mvlm_device* dev, int M, int count, const mvlm_gemv_desc* descs, mvlm_event** ev);
+/* The grouped launches with a fused epilogue per entry: eps[i] (NULL = no
+ * epilogue for any entry) is applied to entry i's output as in mvlm_gemv_ex,
+ * with bias [N_i] and mul / residual [M][N_i] in entry i's y dtype.  This fuses
+ * the bias, GELU and residual adds around the projections of one block
+ * (moondream2.cpp:369-509; activations.cl:66-118, 259-290) into the launch. */
+int mvlm_gemv_grouped_ex(mvlm_device* dev, int count, const mvlm_gemv_desc* descs, const mvlm_epilogue* eps,
+                         mvlm_event** ev);
+int mvlm_gemm_quant_grouped_ex(mvlm_device* dev, int M, int count, const mvlm_gemv_desc* descs,
+                               const mvlm_epilogue* eps, mvlm_event** ev);
 
 /* ---- dequantizing GEMV / skinny GEMM (planned in README.md:57, PLAN.md:65) */
 /* y[N] = x[K] * W^T, W packed Q8_0, x and y fp32. */
@@ -319,6 +328,10 @@ int mvlm_plan_add_gemv(mvlm_plan* plan, const mvlm_buffer* x, int x_dtype, const
                        mvlm_buffer* y, int y_dtype, int M);
 int mvlm_plan_add_gemv_grouped(mvlm_plan* plan, int count, const mvlm_gemv_desc* descs);
 int mvlm_plan_add_gemm_quant_grouped(mvlm_plan* plan, int M, int count, const mvlm_gemv_desc* descs);
+/* plan entries of mvlm_gemv_grouped_ex / mvlm_gemm_quant_grouped_ex */
+int mvlm_plan_add_gemv_grouped_ex(mvlm_plan* plan, int count, const mvlm_gemv_desc* descs, const mvlm_epilogue* eps);
+int mvlm_plan_add_gemm_quant_grouped_ex(mvlm_plan* plan, int M, int count, const mvlm_gemv_desc* descs,
+                                        const mvlm_epilogue* eps);
 /* plan entries with a fused epilogue (mvlm_gemv_ex, M == 1; mvlm_gemm_packed_ex) */
 int mvlm_plan_add_gemv_ex(mvlm_plan* plan, const mvlm_buffer* x, int x_dtype, const mvlm_weight* W,
                           mvlm_buffer* y, int y_dtype, const mvlm_epilogue* ep);

@@ -219,7 +219,8 @@ hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const*
 // Skinny GEMM over up to 8 independent problems (quantized weights of one
 // dtype, fp32 X [M][K] and Y [M][N] each, 1 <= M <= 16) in one launch.
 hipError_t launch_gemm_skinny_group(hipStream_t s, int M, int count, const float* const* Xs,
-                                    const mvlm_weight* const* ws, float* const* Ys, int num_cus);
+                                    const mvlm_weight* const* ws, float* const* Ys, int num_cus,
+                                    const Epilogue* eps = nullptr);
 inline int64_t weight_row_bytes(const mvlm_weight* w) { return is_dense(w->dtype) ? w->ld * (int64_t)dtype_size(w->dtype) : w->ld; }
 // MFMA GEMM.  Its workspace (gemm_workspace_bytes) holds the fp32 partials
 // of a K split (chosen by the launcher's cost model) and zero-padded copies of

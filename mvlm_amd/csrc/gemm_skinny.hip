@@ -403,7 +403,8 @@ hipError_t launch_gemm_skinny(hipStream_t s, const float* X, const mvlm_weight* 
 }
 
 hipError_t launch_gemm_skinny_group(hipStream_t s, int M, int count, const float* const* Xs,
-                                    const mvlm_weight* const* ws, float* const* Ys, int num_cus) {
+                                    const mvlm_weight* const* ws, float* const* Ys, int num_cus,
+                                    const Epilogue* eps) {
     if (M < 1 || M > 16 || count < 1 || count > SKINNY_MAX_GROUP) return hipErrorInvalidValue;
     if (num_cus <= 0) num_cus = 256;
     SkinnyGroup g{};
@@ -413,6 +414,10 @@ hipError_t launch_gemm_skinny_group(hipStream_t s, int M, int count, const float
         const mvlm_weight* W = ws[i];
         if (W->K % 32 != 0 || !is_quant(W->dtype) || W->dtype != ws[0]->dtype) return hipErrorInvalidValue;
         g.p[i] = skinny_problem(Xs[i], W, Ys[i]);
+        if (eps && eps[i].any()) {
+            g.p[i].ep = eps[i];
+            g.p[i].ep_on = 1;
+        }
     }
     if (ws[0]->dtype == MVLM_Q4_0) return launch_skinny_shape<true>(s, g, num_cus);
     return launch_skinny_shape<false>(s, g, num_cus);

@@ -36,6 +36,7 @@ struct Op {
     const mvlm_weight* gw[MVLM_MAX_GROUP] = {};
     void* gy[MVLM_MAX_GROUP] = {};
     int gyd[MVLM_MAX_GROUP] = {};
+    Epilogue gep[MVLM_MAX_GROUP]; // per-entry epilogues of a grouped launch
     Epilogue ep;                  // fused epilogue (GEMM MFMA, GEMV)
     // attention: M = seq_q, N = seq_kv, batch = heads, K = head_dim
     int causal = 0;
@@ -309,11 +310,12 @@ int make_gemv_group(mvlm_device* dev, int M, int count, const mvlm_gemv_desc* de
 // M > 1: the streaming kernel while every entry fits it (M <= 4), else the
 // matrix-core skinny kernel.
 static hipError_t launch_group_op(hipStream_t s, const Op& op) {
-    if (op.M == 1) return launch_gemv_stream_group(s, op.gcount, op.gx, op.a_dtype, op.gw, op.gy, op.gyd, op.num_cus);
+    if (op.M == 1)
+        return launch_gemv_stream_group(s, op.gcount, op.gx, op.a_dtype, op.gw, op.gy, op.gyd, op.num_cus, op.gep);
     bool stream = op.M <= 4;
     for (int i = 0; i < op.gcount && stream; ++i) stream = stream_supported(op.gw[i], op.M);
     if (stream)
-        return launch_gemv_stream_group(s, op.gcount, op.gx, op.a_dtype, op.gw, op.gy, op.gyd, op.num_cus, nullptr,
+        return launch_gemv_stream_group(s, op.gcount, op.gx, op.a_dtype, op.gw, op.gy, op.gyd, op.num_cus, op.gep,
                                         op.M);
     const float* xs[MVLM_MAX_GROUP];
     float* ys[MVLM_MAX_GROUP];
@@ -321,7 +323,17 @@ static hipError_t launch_group_op(hipStream_t s, const Op& op) {
         xs[i] = (const float*)op.gx[i];
         ys[i] = (float*)op.gy[i];
     }
-    return launch_gemm_skinny_group(s, op.M, op.gcount, xs, op.gw, ys, op.num_cus);
+    return launch_gemm_skinny_group(s, op.M, op.gcount, xs, op.gw, ys, op.num_cus, op.gep);
+}
+
+// Per-entry epilogues of a grouped op (eps may be null: none).
+int make_group_epilogues(mvlm_device* dev, const mvlm_epilogue* eps, const char* fn, Op* op) {
+    if (!eps) return MVLM_OK;
+    for (int i = 0; i < op->gcount; ++i) {
+        const int st = make_epilogue(dev, &eps[i], op->M, op->gw[i]->N, op->gyd[i], fn, &op->gep[i]);
+        if (st != MVLM_OK) return st;
+    }
+    return MVLM_OK;
 }
 
 hipError_t enqueue_op(hipStream_t s, const Op& op) {
@@ -469,6 +481,19 @@ extern "C" int mvlm_gemm_quant_grouped(mvlm_device* dev, int M, int count, const
     RUN(make_gemv_group(dev, M, count, descs, fn, &op, true));
 }
 
+extern "C" int mvlm_gemv_grouped_ex(mvlm_device* dev, int count, const mvlm_gemv_desc* descs,
+                                    const mvlm_epilogue* eps, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(then(make_gemv_group(dev, 1, count, descs, fn, &op), [&] { return make_group_epilogues(dev, eps, fn, &op); }));
+}
+
+extern "C" int mvlm_gemm_quant_grouped_ex(mvlm_device* dev, int M, int count, const mvlm_gemv_desc* descs,
+                                          const mvlm_epilogue* eps, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(then(make_gemv_group(dev, M, count, descs, fn, &op, true),
+             [&] { return make_group_epilogues(dev, eps, fn, &op); }));
+}
+
 extern "C" int mvlm_gemv_q8_0(mvlm_device* dev, const mvlm_buffer* x, const mvlm_weight* W, mvlm_buffer* y,
                               int N, int K, mvlm_event** ev) {
     const char* fn = __func__;
@@ -611,6 +636,26 @@ extern "C" int mvlm_plan_add_gemm_quant_grouped(mvlm_plan* plan, int M, int coun
     REQUIRE(plan, "%s: null argument", fn);
     Op op{};
     int st = make_gemv_group(plan->dev, M, count, descs, fn, &op, true);
+    return st != MVLM_OK ? st : plan_push(plan, op);
+}
+
+extern "C" int mvlm_plan_add_gemv_grouped_ex(mvlm_plan* plan, int count, const mvlm_gemv_desc* descs,
+                                             const mvlm_epilogue* eps) {
+    const char* fn = __func__;
+    REQUIRE(plan, "%s: null argument", fn);
+    Op op{};
+    int st = make_gemv_group(plan->dev, 1, count, descs, fn, &op);
+    if (st == MVLM_OK) st = make_group_epilogues(plan->dev, eps, fn, &op);
+    return st != MVLM_OK ? st : plan_push(plan, op);
+}
+
+extern "C" int mvlm_plan_add_gemm_quant_grouped_ex(mvlm_plan* plan, int M, int count, const mvlm_gemv_desc* descs,
+                                                   const mvlm_epilogue* eps) {
+    const char* fn = __func__;
+    REQUIRE(plan, "%s: null argument", fn);
+    Op op{};
+    int st = make_gemv_group(plan->dev, M, count, descs, fn, &op, true);
+    if (st == MVLM_OK) st = make_group_epilogues(plan->dev, eps, fn, &op);
     return st != MVLM_OK ? st : plan_push(plan, op);
 }
 

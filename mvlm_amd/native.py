@@ -109,6 +109,10 @@ _SIGNATURES = {
     "mvlm_plan_add_gemm_packed_ex": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, POINTER(Epilogue)]),
     "mvlm_plan_add_gemv_grouped": (c_int, [_P, c_int, POINTER(GemvDesc)]),
     "mvlm_gemm_quant_grouped": (c_int, [_P, c_int, c_int, POINTER(GemvDesc), _PP]),
+    "mvlm_gemv_grouped_ex": (c_int, [_P, c_int, POINTER(GemvDesc), POINTER(Epilogue), _PP]),
+    "mvlm_gemm_quant_grouped_ex": (c_int, [_P, c_int, c_int, POINTER(GemvDesc), POINTER(Epilogue), _PP]),
+    "mvlm_plan_add_gemv_grouped_ex": (c_int, [_P, c_int, POINTER(GemvDesc), POINTER(Epilogue)]),
+    "mvlm_plan_add_gemm_quant_grouped_ex": (c_int, [_P, c_int, c_int, POINTER(GemvDesc), POINTER(Epilogue)]),
     "mvlm_plan_add_gemm_quant_grouped": (c_int, [_P, c_int, c_int, POINTER(GemvDesc)]),
     "mvlm_gemv_q8_0": (c_int, [_P, _P, _P, _P, c_int, c_int, _PP]),
     "mvlm_gemv_q4_0": (c_int, [_P, _P, _P, _P, c_int, c_int, _PP]),
@@ -278,6 +282,14 @@ class Weight:
         self.dev.sync()
         return out.download(np.float32).reshape(n, k)
 
+    def dequant_rows(self, rows, scratch: "Buffer") -> np.ndarray:
+        """fp32 values of the given rows: the whole weight is dequantized on the
+        device into `scratch` (at least N*K*4 bytes), only those rows come back."""
+        n, k = self.shape
+        _call("mvlm_weight_dequant", self.dev.handle, self.handle, scratch.handle, None)
+        self.dev.sync()
+        return np.stack([scratch.download(np.float32, k, int(r) * k * 4) for r in rows])
+
     def free(self) -> None:
         if self.handle:
             _call("mvlm_weight_free", self.handle)
@@ -381,6 +393,17 @@ def _descs(entries):
     return arr
 
 
+def _epilogues(epilogues, n):
+    """per-entry epilogues: a list of dicts (keys bias, act, mul, residual) or None"""
+    arr = (Epilogue * max(1, n))()
+    keep = []
+    for i, e in enumerate(epilogues):
+        if e:
+            arr[i] = _epilogue(e.get("bias"), e.get("act", ACT_NONE), e.get("mul"), e.get("residual"))
+            keep += [v for k, v in e.items() if k != "act" and v is not None]
+    return arr, keep
+
+
 class Plan:
     """A recorded launch sequence run from native code (eagerly or as a HIP graph).
     Keeps references to the buffers and weights it names so they outlive it."""
@@ -400,18 +423,29 @@ class Plan:
         self._keep += [x, W, y]
         return self
 
-    def add_gemv_grouped(self, entries):
-        """entries: [(x, x_dtype, W, y, y_dtype), ...] served by one launch."""
+    def add_gemv_grouped(self, entries, epilogues=None):
+        """entries: [(x, x_dtype, W, y, y_dtype), ...] served by one launch;
+        epilogues: optional per-entry dicts (bias, act, mul, residual)."""
         arr = _descs(entries)
-        _call("mvlm_plan_add_gemv_grouped", self.handle, len(entries), arr)
+        if epilogues is None:
+            _call("mvlm_plan_add_gemv_grouped", self.handle, len(entries), arr)
+        else:
+            eps, keep = _epilogues(epilogues, len(entries))
+            _call("mvlm_plan_add_gemv_grouped_ex", self.handle, len(entries), arr, eps)
+            self._keep += keep
         for x, _, W, y, _ in entries:
             self._keep += [x, W, y]
         return self
 
-    def add_gemm_quant_grouped(self, M, entries):
+    def add_gemm_quant_grouped(self, M, entries, epilogues=None):
         """entries: [(X, F32, W, Y, F32), ...] of M-row products over Q8_0 / Q4_0 weights, one launch."""
         arr = _descs(entries)
-        _call("mvlm_plan_add_gemm_quant_grouped", self.handle, M, len(entries), arr)
+        if epilogues is None:
+            _call("mvlm_plan_add_gemm_quant_grouped", self.handle, M, len(entries), arr)
+        else:
+            eps, keep = _epilogues(epilogues, len(entries))
+            _call("mvlm_plan_add_gemm_quant_grouped_ex", self.handle, M, len(entries), arr, eps)
+            self._keep += keep
         for x, _, W, y, _ in entries:
             self._keep += [x, W, y]
         return self
@@ -581,13 +615,20 @@ class Device:
     def gemv(self, x, x_dtype, W, y, y_dtype, N, K, event=False):
         return self._launch("mvlm_gemv", (x.handle, x_dtype, W.handle, y.handle, y_dtype, N, K), event)
 
-    def gemv_grouped(self, entries, event=False):
-        """entries: [(x, x_dtype, W, y, y_dtype), ...], one launch for all."""
-        return self._launch("mvlm_gemv_grouped", (len(entries), _descs(entries)), event)
+    def gemv_grouped(self, entries, event=False, epilogues=None):
+        """entries: [(x, x_dtype, W, y, y_dtype), ...], one launch for all;
+        epilogues: optional per-entry dicts (bias, act, mul, residual)."""
+        if epilogues is None:
+            return self._launch("mvlm_gemv_grouped", (len(entries), _descs(entries)), event)
+        eps, _ = _epilogues(epilogues, len(entries))
+        return self._launch("mvlm_gemv_grouped_ex", (len(entries), _descs(entries), eps), event)
 
-    def gemm_quant_grouped(self, M, entries, event=False):
+    def gemm_quant_grouped(self, M, entries, event=False, epilogues=None):
         """entries: [(X, F32, W, Y, F32), ...]: Y = X W^T for each, M rows, one launch."""
-        return self._launch("mvlm_gemm_quant_grouped", (M, len(entries), _descs(entries)), event)
+        if epilogues is None:
+            return self._launch("mvlm_gemm_quant_grouped", (M, len(entries), _descs(entries)), event)
+        eps, _ = _epilogues(epilogues, len(entries))
+        return self._launch("mvlm_gemm_quant_grouped_ex", (M, len(entries), _descs(entries), eps), event)
 
     def gemv_q8_0(self, x, W, y, N, K, event=False):
         return self._launch("mvlm_gemv_q8_0", (x.handle, W.handle, y.handle, N, K), event)

@@ -1,0 +1,89 @@
+"""The decode-step plans bench.py times, checked end to end on the GPU.
+
+bench.build_decode_plan and bench.build_token_plan are the exact plans of the
+benchmark's headline step (Phi-1.5, 24 layers of {QKV 2048->6144, dense
+2048->2048, fc1 2048->8192, fc2 8192->2048} + LM head 2048->51200, grouped
+into 49 launches, replayed as a HIP graph; moondream2.cpp:359-541 is the
+reference's sequence of these projections).  After graph replays every one of
+the 97 outputs is compared with the oracle's fp32 GEMV (exact dequantization,
+fp32 fma chain in ascending k) on 256 rows spread over the output, within
+1e-5 * S (S = sum_k |x_k w_k|); the token pick at the end of the decode-token
+plan must be the oracle's argmax of the LM head's logits."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import bench
+import mvlm_amd as m
+
+pytestmark = pytest.mark.gpu
+
+ROWS = 256
+
+
+def sample_rows(N):
+    return np.unique(np.linspace(0, N - 1, ROWS).astype(np.int64))
+
+
+def check_outputs(dev, orc, weights, io, M):
+    """every GEMV output (sampled rows) against the oracle; with io["ep"], the
+    output is the epilogue (bias, GELU, residual) applied in fp64 to the fp64
+    product, within the accumulator bound carried through it plus fp32 ulps"""
+    scratch = dev.alloc(max(N * K for _, N, K in bench.PHI_STEP) * 4)
+    xs = {name: io["x"][name].download(np.float32, M * K).reshape(M, K) for name, _, K in bench.PHI_STEP[:4]}
+    eps = io.get("ep") or [None] * len(bench.PHI_STEP)
+    for i, ((name, N, K), W, y, ep) in enumerate(zip(bench.PHI_STEP, weights, io["y"], eps)):
+        x = xs["qkv" if name == "lm_head" else name]
+        rows = sample_rows(N)
+        deq = W.dequant_rows(rows, scratch)                          # [rows, K] fp32, exact
+        got = y.download(np.float32, M * N).reshape(M, N)[:, rows].astype(np.float64)
+        if ep is None:
+            ref = orc.gemm_nk("f32", np.ascontiguousarray(x), np.ascontiguousarray(deq), M, len(rows), K)
+            _, S = orc.gemm_f64(x.astype(np.float64), deq.astype(np.float64), M, len(rows), K)
+            err = np.abs(got - ref.reshape(M, len(rows)))
+            assert np.all(err <= 1e-5 * S), (i, name, float(np.max(err / (1e-5 * S))))
+            continue
+        Y64, S = orc.gemm_f64(x.astype(np.float64), deq.astype(np.float64), M, len(rows), K)
+        bias = ep["bias"].download(np.float32, N)[rows].astype(np.float64) if ep.get("bias") else None
+        res = (ep["residual"].download(np.float32, M * N).reshape(M, N)[:, rows].astype(np.float64)
+               if ep.get("residual") else None)
+        act = ep.get("act", 0)
+        ref = orc.epilogue_f64(Y64, bias, None, res, act)
+        body = orc.epilogue_f64(Y64, bias, act=act)
+        tol = 1e-5 * S * 1.2 + 4e-6 * (np.abs(body) + (np.abs(res) if res is not None else 0.0)) + 1e-30
+        err = np.abs(got - ref)
+        assert np.all(err <= tol), (i, name, float(np.max(err / tol)))
+    return xs
+
+
+@pytest.mark.parametrize("qt,M", [("q8_0", 1), ("q4_0", 1), ("q4_0", 4), ("q8_0", 4), ("q4_0", 16)])
+def test_decode_step_plan_outputs(dev, orc, qt, M):
+    print(f"[decode plan] {qt} M={M}", flush=True)
+    plan, weights, grouped, io = bench.build_decode_plan(dev, m, qt, M, True)
+    assert grouped and len(plan) == 49
+    for y in io["y"]:
+        y.zero()
+    plan.use_graph(True)
+    plan.run(3)
+    dev.sync()
+    check_outputs(dev, orc, weights, io, M)
+    plan.destroy()
+    for W in weights:
+        W.free()
+
+
+def test_decode_token_plan_picks_the_argmax(dev, orc):
+    print("[token plan] q8_0 cache 512", flush=True)
+    plan, weights, io = bench.build_token_plan(dev, m, "q8_0", 512)
+    assert len(plan) == 24 * 3 + 2
+    plan.use_graph(True)
+    plan.run(2)
+    dev.sync()
+    check_outputs(dev, orc, weights, io, 1)
+    logits = io["y"][-1].download(np.float32, 51200)
+    want = orc.argmax(logits, m.F32, 1, 51200, 51200)[0]
+    assert int(io["token"].download(np.int32, 1)[0]) == int(want)
+    plan.destroy()
+    for W in weights:
+        W.free()

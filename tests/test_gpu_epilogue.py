@@ -173,6 +173,55 @@ def test_dense_gemv_epilogue(dev, orc, yd, wd, N, K):
     check(orc, got, Y64, S, vals, GELU, yd, 1e-5)
 
 
+@pytest.mark.parametrize("qt", [m.Q8_0, m.Q4_0])
+@pytest.mark.parametrize("M", [1, 3, 16])
+def test_grouped_epilogues(dev, orc, qt, M):
+    """One grouped launch applying a different epilogue per entry, like a Phi-1.5
+    block's projections: QKV + bias, fc1 + bias + GELU, dense + bias + residual,
+    fc2 + bias + residual written in place.  M = 1 and 3 run the streaming kernel,
+    M = 16 the skinny kernel; the plan entry gives the direct call's bits."""
+    shapes = [(384, 2048, dict(bias=True)), (512, 2048, dict(bias=True, act=GELU)),
+              (256, 1024, dict(bias=True, residual=True)), (130, 8192, dict(bias=True, residual=True, inplace=True))]
+    deq = orc.dequant_q8_0 if qt == m.Q8_0 else orc.dequant_q4_0
+    gen = orc.q8_0_blocks if qt == m.Q8_0 else orc.q4_0_blocks
+    entries, eps, checks, outs = [], [], [], []
+    for i, (N, K, spec) in enumerate(shapes):
+        X = orc.normal_f32(M * K, 0xA0 + i)
+        blocks = gen(N * K // 32, 0xB0 + i)
+        W = dev.pack(blocks, qt, N, K)
+        ops, vals = make_operands(dev, orc, M, N, F32, 0xC0 + i, spec.get("bias", False), False,
+                                  spec.get("residual", False))
+        y = ops["residual"] if spec.get("inplace") else dev.alloc(M * N * 4)
+        entries.append((dev.upload(X), F32, W, y, F32))
+        eps.append({"bias": ops["bias"], "act": spec.get("act", NONE), "residual": ops["residual"]})
+        Y64, S = orc.gemm_f64(X.astype(np.float64).reshape(M, K), deq(blocks).astype(np.float64).reshape(N, K),
+                              M, N, K)
+        checks.append((Y64, S, vals, spec.get("act", NONE)))
+        outs.append(y)
+    # a plan copy first (in-place residual: it must read the residual before the direct call overwrites it)
+    plan_outs = [dev.alloc(M * N * 4) for N, _, _ in shapes]
+    plan_res = [dev.upload(e[3].download(np.float32)) if shapes[i][2].get("inplace") else None
+                for i, e in enumerate(entries)]
+    plan_entries = [(x, xd, W, plan_res[i] if plan_res[i] is not None else plan_outs[i], yd)
+                    for i, (x, xd, W, _, yd) in enumerate(entries)]
+    plan_eps = [dict(e, residual=plan_res[i]) if plan_res[i] is not None else e for i, e in enumerate(eps)]
+    plan = m.Plan(dev)
+    if M == 1:
+        plan.add_gemv_grouped(plan_entries, epilogues=plan_eps)
+        dev.gemv_grouped(entries, epilogues=eps)
+    else:
+        plan.add_gemm_quant_grouped(M, plan_entries, epilogues=plan_eps)
+        dev.gemm_quant_grouped(M, entries, epilogues=eps)
+    plan.run(1)
+    dev.sync()
+    for i, ((N, K, spec), y, (Y64, S, vals, act)) in enumerate(zip(shapes, outs, checks)):
+        got = y.download(np.float32, M * N).astype(np.float64).reshape(M, N)
+        check(orc, got, Y64, S, vals, act, F32, 1e-5)
+        py = plan_res[i] if plan_res[i] is not None else plan_outs[i]
+        assert np.array_equal(py.download(np.float32, M * N), y.download(np.float32, M * N)), i
+    plan.destroy()
+
+
 def test_plan_epilogues_match_direct_calls(dev, orc):
     M, N, K = 33, 64, 2048
     A = orc.normal_f16(M * K, 0x7D)

@@ -165,6 +165,21 @@ def test_gemv_exact_bit_exact(dev, orc, N, K):
     assert np.array_equal(got, ref16), int(np.sum(got != ref16))
 
 
+def test_gemv_exact_summation_order_fixture(dev):
+    """the hand-built fold-order cases (tests/golden/gemv_fold_order.json): only
+    the reference gemv's k partition, per-item order and fold pairs give these bits"""
+    import json
+    import os
+    path = os.path.join(os.path.dirname(__file__), "golden", "gemv_fold_order.json")
+    for case in json.load(open(path))["cases"]:
+        K, N = case["K"], case["N"]
+        W = dev.pack(np.array(case["W_kn"], np.uint16), F16, N, K, layout=m.LAYOUT_KN)
+        x = dev.upload(np.array(case["x"], np.uint16))
+        y = dev.alloc(N * 2)
+        dev.gemv_exact(x, W, y, N, K)
+        assert y.download(np.uint16).tolist() == case["y_bits"], case["name"]
+
+
 def test_gemv_exact_errors(dev, orc):
     B = orc.normal_f16(32 * 8, 143)
     W = dev.pack(B, F16, 8, 32, layout=m.LAYOUT_KN)

@@ -172,6 +172,24 @@ def test_gemv_against_fp64_and_naive(orc):
     assert within(y32, n32[0], scale[0], 1e-6)[0]
 
 
+def gemv_fold_cases():
+    path = os.path.join(os.path.dirname(__file__), "golden", "gemv_fold_order.json")
+    return json.load(open(path))["cases"]
+
+
+@pytest.mark.parametrize("case", gemv_fold_cases(), ids=lambda c: c["name"])
+def test_gemv_summation_order_fixture(orc, case):
+    """Hand-built inputs whose fp16 result only the reference gemv's order gives
+    (strided k partition, ascending k per work item, fold pairs 128..1;
+    tests/golden/make_gemv_fold_fixture.py derives each expected value)"""
+    K, N = case["K"], case["N"]
+    x = np.array(case["x"], np.uint16)
+    W = np.array(case["W_kn"], np.uint16)
+    y16, _ = orc.gemv(x, W, N, K)
+    assert y16.tolist() == case["y_bits"], case["name"]
+    assert case["y_bits"] != case["other_bits"]          # the case separates the two orders
+
+
 def test_closed_forms(orc):
     K, N = 96, 40
     B = orc.normal_f16(K * N, 51, 0.5)
