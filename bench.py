@@ -49,6 +49,14 @@ def gemv_bytes(qt, N, K, M):
     return quant_bytes(qt, N, K) + 4 * M * K + 4 * M * N
 
 
+def roofline(bound, achieved, timing):
+    """roofline block of one workload: achieved GB/s (bound "hbm") or TFLOP/s
+    (bound "mfma") against MI355X's nominal peak"""
+    peak, unit = (PEAK_HBM_GBS, "GB/s") if bound == "hbm" else (PEAK_F16_TFLOPS, "TFLOP/s")
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "timing": timing}
+
+
 def timed_plan(dev, plan, steps, warmup):
     """Wall-clock device time of `steps` plan runs after `warmup` runs (ms per run)."""
     plan.run(warmup)
@@ -142,6 +150,7 @@ def decode_step(dev, m, qt, M, steps, warmup, graph=True, grouped=True):
     }
     res["frac"] = res["gbs"] / PEAK_HBM_GBS
     res["kernel_frac"] = res["kernel_gbs"] / PEAK_HBM_GBS
+    res["roofline"] = roofline("hbm", res["gbs"], "timed region (HIP events around the graph replays) / launches")
     plan.destroy()
     for W in weights:
         W.free()
@@ -259,6 +268,7 @@ def gemm_shape(dev, m, name, M, N, K, steps, warmup):
     res = {"workload": name, "shape": [M, N, K], "us": ms * 1e3, "tflops": flops / ms / 1e9,
            "kernel_us": float(per_op[0]) * 1e3}
     res["frac"] = res["tflops"] / PEAK_F16_TFLOPS
+    res["roofline"] = roofline("mfma", res["tflops"], "timed region (HIP events around the graph replays) / launches")
     plan.destroy()
     return res
 
@@ -340,6 +350,58 @@ def token_pick(dev, m, steps, warmup):
     return res
 
 
+# benchmarks/gemm_bench.cpp:16-22: name, M, K, N
+GEMM_BENCH_CONFIGS = (("small", 256, 256, 256), ("medium", 2048, 2048, 2048), ("decode_gemv", 1, 2048, 2048),
+                      ("llm_ffn", 1, 2048, 8192), ("prefill_32", 32, 2048, 2048))
+GEMM_BENCH_VARIANTS = ("naive", "tiled", "image", "gemv", "gemv_exact")
+
+
+def gemm_bench_matrix(dev, m, warmup=5, iters=20):
+    """The reference bench's variant x config table (gemm_bench.cpp:16-22, 58-63,
+    141-186): fp16 A[M,K] and B[K,N] (the reference's row-major B), fp16 C;
+    naive / tiled (the reference kernels' exact fma order), image (the MFMA
+    GEMM on B packed from the reference's [K,N] layout), gemv and gemv_exact
+    (M = 1 only).  5 warmup launches, then 20 launches each timed by its own
+    start/stop events; GFLOP/s = 2MKN / average time (gemm_bench.cpp:48-51),
+    efficiency against the 2.5 PFLOP/s dense fp16 peak; GEMV rows also give
+    GB/s over the fp16 weight + x + y bytes.  The same matrices are reused
+    launch after launch, as in the reference bench, so they sit in the
+    256 MB Infinity Cache."""
+    rows = []
+    for cname, M, K, N in GEMM_BENCH_CONFIGS:
+        A = dev.fill_normal(dev.alloc(M * K * 2), m.F16, M * K, SEED ^ 0x801, 1.0)
+        B = dev.fill_normal(dev.alloc(K * N * 2), m.F16, K * N, SEED ^ 0x802, 0.02)
+        C = dev.alloc(M * N * 2)
+        W = dev.pack(B.download(np.uint16, K * N), m.F16, N, K, layout=m.LAYOUT_KN)
+        launch = {"naive": lambda ev: dev.gemm_naive(A, B, C, M, N, K, event=ev),
+                  "tiled": lambda ev: dev.gemm_tiled(A, B, C, M, N, K, event=ev),
+                  "image": lambda ev: dev.gemm_packed(A, m.F16, W, C, m.F16, M, N, K, event=ev),
+                  "gemv": lambda ev: dev.gemv(A, m.F16, W, C, m.F16, N, K, event=ev),
+                  "gemv_exact": lambda ev: dev.gemv_exact(A, W, C, N, K, event=ev)}
+        for v in GEMM_BENCH_VARIANTS:
+            if v.startswith("gemv") and M != 1:
+                continue
+            for _ in range(warmup):
+                launch(False)
+            dev.sync()
+            ts = []
+            for _ in range(iters):
+                ev = launch(True)
+                ev.wait()
+                ts.append(ev.elapsed_ms())
+            avg = float(np.mean(ts))
+            gf = 2.0 * M * K * N / (avg * 1e6)
+            r = {"variant": v, "config": cname, "M": M, "K": K, "N": N, "avg_ms": avg, "min_ms": float(min(ts)),
+                 "max_ms": float(max(ts)), "gflops": gf, "eff_pct_of_2.5PF": 100.0 * gf / (PEAK_F16_TFLOPS * 1e3)}
+            if M == 1:
+                r["gbs"] = (2.0 * K * N + 2 * K + 2 * N) / (avg * 1e6)
+            rows.append(r)
+            log(f"[bench]   {v:10s} {cname:12s} {M:4d}x{K:4d}x{N:4d} {avg:8.4f} ms {gf:10.1f} GFLOPS "
+                f"{r['eff_pct_of_2.5PF']:5.2f}% eff" + (f" {r['gbs']:7.0f} GB/s" if M == 1 else ""))
+        W.free()
+    return rows
+
+
 GEMM_SHAPES = (("phi15_prefill_qkv", 768, 6144, 2048), ("phi15_prefill_fc1", 768, 8192, 2048),
                ("phi15_prefill_fc2", 768, 2048, 8192), ("siglip_qkv", 729, 3456, 1152),
                ("siglip_out", 729, 1152, 1152), ("siglip_fc1", 729, 4304, 1152),
@@ -399,7 +461,47 @@ def cpu_baseline(seconds=10.0):
                       f"{nbytes / 1e6:.1f} MB each pass) in {dt:.1f} s: dequantize each 32-block exactly, "
                       f"fp32 fma over ascending k, OpenMP over rows",
             "single_thread_value": nbytes * reps1 / dt1 / 1e9,
-            "single_thread_sample": f"{reps1} passes of the same layer on 1 thread in {dt1:.1f} s"}
+            "single_thread_sample": f"{reps1} passes of the same layer on 1 thread in {dt1:.1f} s",
+            "legs": cpu_reference_legs(threads)}
+
+
+def _timed(fn, seconds):
+    """calls fn until `seconds` have passed (at least twice, the first untimed); returns (calls, s)"""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while n < 1 or time.perf_counter() - t0 < seconds:
+        fn()
+        n += 1
+    return n, time.perf_counter() - t0
+
+
+def cpu_reference_legs(threads, seconds=1.5):
+    """The oracle's restatements of the reference kernels themselves, timed on the
+    host in the units of their GPU rows: gemv (gemm.cl:219-270, fp16 x and W, the
+    256-item partition and fold) at the fp32 GEMV's shape 1x2048x8192; the fp32
+    NT GEMV (C1: x[2048] fp32, W[8192][2048] fp32, ascending-k fma); gemm_image
+    (gemm.cl:157-200) on a slice of 4 rows per thread of the Phi-1.5 QKV prefill
+    GEMM (768x6144x2048: each row is an independent work item, so the rate
+    carries over).  Each on all `threads` and on one thread."""
+    from oracle import oracle_ffi as orc
+    legs = []
+    K, N = 2048, 8192
+    x16, B16 = orc.normal_f16(K, SEED ^ 0x901), orc.normal_f16(K * N, SEED ^ 0x902, 0.02)
+    x32, W32 = orc.normal_f32(K, SEED ^ 0x903), orc.normal_f32(N * K, SEED ^ 0x904, 0.02)
+    Nq, Kq = 6144, 2048
+    Aq, Bq = orc.normal_f16(4 * threads * Kq, SEED ^ 0x905), orc.normal_f16(Kq * Nq, SEED ^ 0x906, 0.02)
+    for nt in (threads, 1):
+        Mq = 4 * nt
+        n, dt = _timed(lambda: orc.gemv(x16, B16, N, K, nthreads=nt), seconds)
+        legs.append({"kernel": "gemv (gemm.cl:219-270)", "shape": "1x2048x8192 fp16", "threads": nt,
+                     "gbs": (2.0 * K * N + 2 * K + 2 * N) * n / dt / 1e9, "us": dt / n * 1e6})
+        n, dt = _timed(lambda: orc.gemm_nk("f32", x32, W32, 1, N, K, nt), seconds)
+        legs.append({"kernel": "fp32 NT GEMV (C1)", "shape": "1x2048x8192 fp32", "threads": nt,
+                     "gbs": (4.0 * K * N + 4 * K + 4 * N) * n / dt / 1e9, "us": dt / n * 1e6})
+        n, dt = _timed(lambda: orc.gemm_image_mt(Aq, Bq, Mq, Nq, Kq, nt), seconds)
+        legs.append({"kernel": "gemm_image (gemm.cl:157-200)", "shape": f"{Mq}x6144x2048 slice of 768x6144x2048 fp16",
+                     "threads": nt, "gflops": 2.0 * Mq * Nq * Kq * n / dt / 1e9, "ms": dt / n * 1e3})
+    return legs
 
 
 # ---------------------------------------------------------------------------
@@ -582,6 +684,8 @@ def main():
                     help="only the attention and token-pick workloads (one JSON line of them)")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the prefill / vision GEMM shapes and the batched QK^T (one JSON line of them)")
+    ap.add_argument("--gemm-bench", action="store_true",
+                    help="only the reference bench's variant x config table (one JSON line)")
     ap.add_argument("--pmc-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn the two counter runs into " + os.path.relpath(TRAFFIC_FILE, ROOT))
     args = ap.parse_args()
@@ -607,6 +711,10 @@ def main():
     info = dev.info()
     log(f"[bench] {info.device_name.decode()} {info.arch_name.decode()} CUs={info.compute_units} "
         f"clock={info.max_clock_mhz} MHz HBM={info.global_mem_size / 2**30:.0f} GiB")
+    if args.gemm_bench:
+        print(json.dumps({"gemm_bench_matrix": gemm_bench_matrix(dev, m)}), flush=True)
+        dev.close()
+        return
     if args.attention_only or args.gemm_only:
         extra = {}
         if args.gemm_only:
@@ -644,12 +752,17 @@ def main():
             f"({100 * r['frac']:.1f}%; reference summation order)")
         gemm_extras(dev, m, 20, 5, extra)
         f4_extras(dev, m, 20, 5, extra)
+        log("[bench] gemm_bench.cpp's variant x config table")
+        extra["gemm_bench_matrix"] = gemm_bench_matrix(dev, m)
 
     cpu = None
     if not args.no_cpu:
         log("[bench] CPU baseline (oracle Q8_0 GEMV on host cores)")
         cpu = cpu_baseline(args.cpu_seconds)
         log(f"[bench]   {cpu['value']:.2f} GB/s on {cpu['cores']} threads, {cpu['single_thread_value']:.2f} GB/s on 1")
+        for leg in cpu["legs"]:
+            log(f"[bench]   cpu {leg['kernel']} {leg['shape']} on {leg['threads']} threads: "
+                + (f"{leg['gbs']:.2f} GB/s" if "gbs" in leg else f"{leg['gflops']:.2f} GFLOP/s"))
     dev.close()
 
     out = {
@@ -673,14 +786,20 @@ def main():
                    "grouping": "per layer {QKV, fc1} and {dense, fc2} as one launch each (independent in "
                                "Phi-1.5's parallel block); LM head alone",
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(head["kernel_gbs"], 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(head["kernel_frac"], 4), "traffic": measured_traffic(),
+        "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(head["frac"], 4), "traffic": measured_traffic(),
                      "traffic_note": "HBM bytes per step (49 launches) from rocprofv3 FETCH_SIZE + WRITE_SIZE, "
                                      "scaled by a 256 MiB device copy; " + os.path.relpath(TRAFFIC_FILE, ROOT),
                      "kernel": "gemv_stream_kernel<Q8Fmt>",
-                     "timing": f"algorithmic bytes of one step / sum of the {head['launches']} kernel "
-                               "execution times, each from HIP start/stop events on the launch's own dispatch "
-                               "(hipExtLaunchKernelGGL) on the plan's stream, median of 5 eager steps"},
+                     "timing": f"algorithmic bytes of one step / ({head['launches']} x the kernel's average "
+                               "launch duration), the average being the timed region (HIP events on the plan's "
+                               "stream around the graph replays) divided by the launches it holds (every launch "
+                               "of the step is this kernel)",
+                     "kernel_events_us_per_step": round(head["kernel_ms_sum"] * 1e3, 2),
+                     "kernel_events_frac": round(head["kernel_frac"], 4),
+                     "kernel_events_note": "sum of the 49 kernel execution times from HIP start/stop events on "
+                                           "each launch's own dispatch packet, median of 5 eager steps (no "
+                                           "inter-launch gaps)"},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -250,11 +250,14 @@ void orc_gemm_tiled(const uint16_t* A, const uint16_t* B, uint16_t* C16, float* 
  * height K, zero-padding the columns to a multiple of 4; gemm.cl:157-200 then
  * lets each item produce 4 adjacent columns (float4 fma over ascending k) and
  * stores min(4, N - col_base) of them. */
-void orc_gemm_image(const uint16_t* A, const uint16_t* B, uint16_t* C16, float* C32,
-                    int M, int N, int K) {
+void orc_gemm_image_mt(const uint16_t* A, const uint16_t* B, uint16_t* C16, float* C32,
+                       int M, int N, int K, int nthreads) {
     int width = (N + 3) / 4, padded = width * 4;
+    int nt = nthreads > 0 ? nthreads : orc_max_threads();
     uint16_t* img = (uint16_t*)calloc((size_t)K * padded, sizeof(uint16_t));
     for (int k = 0; k < K; ++k) memcpy(img + (size_t)k * padded, B + (size_t)k * N, sizeof(uint16_t) * N);
+    /* rows are independent work items: threads change nothing in the results */
+    #pragma omp parallel for schedule(static) num_threads(nt)
     for (int row = 0; row < M; ++row)
         for (int col4 = 0; col4 < width; ++col4) {
             int col_base = col4 * 4;
@@ -273,14 +276,21 @@ void orc_gemm_image(const uint16_t* A, const uint16_t* B, uint16_t* C16, float* 
     free(img);
 }
 
+void orc_gemm_image(const uint16_t* A, const uint16_t* B, uint16_t* C16, float* C32, int M, int N, int K) {
+    orc_gemm_image_mt(A, B, C16, C32, M, N, K, 1);
+}
+
 /* gemm.cl:215-270 as launched by compute.cpp:141-147: one 256-item group per
  * image column (4 outputs); item lid accumulates k = lid, lid+256, ... with a
  * float4 fma; then scratch[lid] += scratch[lid+stride] for stride = 128..1. */
-void orc_gemv(const uint16_t* x, const uint16_t* B, uint16_t* y16, float* y32, int N, int K) {
+void orc_gemv_mt(const uint16_t* x, const uint16_t* B, uint16_t* y16, float* y32, int N, int K, int nthreads) {
     enum { WG = 256 };
     int width = (N + 3) / 4;
-    float (*scratch)[4] = (float (*)[4])malloc(sizeof(float) * 4 * WG);
+    int nt = nthreads > 0 ? nthreads : orc_max_threads();
+    /* work-groups (4 outputs each) are independent: threads change nothing */
+    #pragma omp parallel for schedule(static) num_threads(nt)
     for (int col4 = 0; col4 < width; ++col4) {
+        float scratch[WG][4];
         int col_base = col4 * 4;
         for (int lid = 0; lid < WG; ++lid) {
             float p[4] = {0.f, 0.f, 0.f, 0.f};
@@ -303,7 +313,10 @@ void orc_gemv(const uint16_t* x, const uint16_t* B, uint16_t* y16, float* y32, i
             if (y32) y32[col_base + c] = scratch[0][c];
         }
     }
-    free(scratch);
+}
+
+void orc_gemv(const uint16_t* x, const uint16_t* B, uint16_t* y16, float* y32, int N, int K) {
+    orc_gemv_mt(x, B, y16, y32, N, K, 1);
 }
 
 /* ------------------------------------------------------------------------ */

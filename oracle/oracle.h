@@ -84,6 +84,10 @@ void orc_gemm_tiled(const uint16_t* A, const uint16_t* B, uint16_t* C16, float* 
 void orc_gemm_image(const uint16_t* A, const uint16_t* B, uint16_t* C16, float* C32,
                     int M, int N, int K);
 void orc_gemv(const uint16_t* x, const uint16_t* B, uint16_t* y16, float* y32, int N, int K);
+/* the same on nthreads OpenMP threads (0: all); bit-identical results */
+void orc_gemm_image_mt(const uint16_t* A, const uint16_t* B, uint16_t* C16, float* C32,
+                       int M, int N, int K, int nthreads);
+void orc_gemv_mt(const uint16_t* x, const uint16_t* B, uint16_t* y16, float* y32, int N, int K, int nthreads);
 
 /* ---- the NT path: W is [N,K] (GGUF-native), y = X * W^T ---------------- */
 /* fp32 fma chain over ascending k per output; OpenMP over rows when

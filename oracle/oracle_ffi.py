@@ -59,6 +59,8 @@ def lib():
             "orc_gemm_tiled": (None, [_u16p, _u16p, _u16p, _f32p, i, i, i]),
             "orc_gemm_image": (None, [_u16p, _u16p, _u16p, _f32p, i, i, i]),
             "orc_gemv": (None, [_u16p, _u16p, _u16p, _f32p, i, i]),
+            "orc_gemm_image_mt": (None, [_u16p, _u16p, _u16p, _f32p, i, i, i, i]),
+            "orc_gemv_mt": (None, [_u16p, _u16p, _u16p, _f32p, i, i, i]),
             "orc_gemm_f32_nk": (None, [_f32p, _f32p, _f32p, i, i, i, i]),
             "orc_gemm_f16_nk": (None, [_u16p, _u16p, _f32p, i, i, i, i]),
             "orc_gemm_bf16_nk": (None, [_u16p, _u16p, _f32p, i, i, i, i]),
@@ -185,12 +187,20 @@ def gemm_image(A, B, M, N, K):
     return _ref_kn(lib().orc_gemm_image, A, B, M, N, K)
 
 
-def gemv(x, B, N, K):
+def gemv(x, B, N, K, nthreads=1):
     y16 = np.empty(N, np.uint16)
     y32 = np.empty(N, np.float32)
-    lib().orc_gemv(np.ascontiguousarray(x, np.uint16).ravel(), np.ascontiguousarray(B, np.uint16).ravel(),
-                   y16, y32, N, K)
+    lib().orc_gemv_mt(np.ascontiguousarray(x, np.uint16).ravel(), np.ascontiguousarray(B, np.uint16).ravel(),
+                      y16, y32, N, K, nthreads)
     return y16, y32
+
+
+def gemm_image_mt(A, B, M, N, K, nthreads=0):
+    C16 = np.empty(M * N, np.uint16)
+    C32 = np.empty(M * N, np.float32)
+    lib().orc_gemm_image_mt(np.ascontiguousarray(A, np.uint16).ravel(), np.ascontiguousarray(B, np.uint16).ravel(),
+                            C16, C32, M, N, K, nthreads)
+    return C16.reshape(M, N), C32.reshape(M, N)
 
 
 def gemm_nk(kind, X, W, M, N, K, nthreads=0):

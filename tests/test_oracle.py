@@ -172,6 +172,20 @@ def test_gemv_against_fp64_and_naive(orc):
     assert within(y32, n32[0], scale[0], 1e-6)[0]
 
 
+def test_threaded_reference_kernels_are_bit_identical(orc):
+    """orc_gemv_mt / orc_gemm_image_mt (the host baseline's threaded runs) give
+    the single-thread restatement's bits"""
+    M, N, K = 9, 70, 300
+    A = orc.normal_f16(M * K, 61)
+    B = orc.normal_f16(K * N, 62, 0.02)
+    c16, c32 = orc.gemm_image(A, B, M, N, K)
+    t16, t32 = orc.gemm_image_mt(A, B, M, N, K, 0)
+    assert np.array_equal(c16, t16) and np.array_equal(c32.view(np.uint32), t32.view(np.uint32))
+    y16, y32 = orc.gemv(A[:K], B, N, K)
+    z16, z32 = orc.gemv(A[:K], B, N, K, nthreads=0)
+    assert np.array_equal(y16, z16) and np.array_equal(y32.view(np.uint32), z32.view(np.uint32))
+
+
 def gemv_fold_cases():
     path = os.path.join(os.path.dirname(__file__), "golden", "gemv_fold_order.json")
     return json.load(open(path))["cases"]
