@@ -2,6 +2,7 @@
 
     python -m mvlm_amd.build            # compile every source, link the library
     python -m mvlm_amd.build --check    # also list the exported mvlm_* symbols
+    python -m mvlm_amd.build --incremental   # recompile only sources newer than their object
 
 The library lands in mvlm_amd/lib/ so it travels with the source tree; the
 object files go to mvlm_amd/_build/.
@@ -42,8 +43,7 @@ def sources():
 
 
 def _compile(src: str) -> str:
-    base = os.path.relpath(src, PKG).replace(os.sep, "_")
-    obj = os.path.join(OBJ, base + ".o")
+    obj = _object(src)
     cmd = [HIPCC, f"--offload-arch={ARCH}", *COMMON]
     if src.endswith(".hip"):
         cmd += ["-x", "hip", *DEVICE_FLAGS]
@@ -58,12 +58,30 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(jobs: int = 8, verbose: bool = True) -> str:
+def _object(src: str) -> str:
+    return os.path.join(OBJ, os.path.relpath(src, PKG).replace(os.sep, "_") + ".o")
+
+
+def _stale(src: str, newest_header: float) -> bool:
+    obj = _object(src)
+    return not os.path.exists(obj) or os.path.getmtime(obj) < max(os.path.getmtime(src), newest_header)
+
+
+def build(jobs: int = 8, verbose: bool = True, incremental: bool = False) -> str:
+    """Compile every source (or, with incremental, those newer than their
+    object file or than any header) and link the library."""
     os.makedirs(OBJ, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
     srcs = sources()
-    with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs)))) as ex:
-        objs = list(ex.map(_compile, srcs))
+    todo = srcs
+    if incremental:
+        headers = [os.path.join(d, f) for d in (CSRC, ENGINE, os.path.join(ROOT, "include"))
+                   for f in os.listdir(d) if f.endswith(".h")]
+        newest = max(os.path.getmtime(h) for h in headers)
+        todo = [s for s in srcs if _stale(s, newest)]
+    with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, max(1, len(todo))))) as ex:
+        list(ex.map(_compile, todo))
+    objs = [_object(s) for s in srcs]
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs,
            "-Wl,-rpath,/opt/rocm/lib", "-Wl,--no-undefined"]
@@ -102,7 +120,8 @@ if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--check", action="store_true")
     ap.add_argument("-j", "--jobs", type=int, default=8)
+    ap.add_argument("--incremental", action="store_true")
     a = ap.parse_args()
-    build(a.jobs)
+    build(a.jobs, incremental=a.incremental)
     if a.check:
         print("\n".join(exported_symbols()))

@@ -36,6 +36,7 @@
 
 #include <cstdio>
 #include <cstdlib>
+#include <type_traits>
 
 namespace mvlm {
 
@@ -68,7 +69,66 @@ struct GemmArgs {
     // gemm_splitk_reduce_kernel (which then applies the epilogue)
     int splits, split_stages;
     float* ws;
+    // 4 consecutive columns of a row start 16-byte (fp32) / 8-byte (16-bit)
+    // aligned in C (vec_c) and in the split partials (vec_ws), so one vector
+    // store writes them
+    int vec_c, vec_ws;
 };
+
+// f(std::integral_constant<int, 0>{}), ..., f(std::integral_constant<int, N - 1>{})
+template <int N, int I = 0, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, I + 1>(f);
+    }
+}
+
+// fp32 partial of 4 consecutive columns (n_left of them below N; the row
+// starts 16-byte aligned)
+__device__ __forceinline__ void store_partial4(float* ws, int64_t i, f32x4 v, int n_left) {
+    if (n_left >= 4) {
+        *reinterpret_cast<f32x4*>(ws + i) = v;
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        if (e < n_left) ws[i + e] = v[e];
+}
+
+// C row `row_off` (element offset of the row), columns col..col+3: epilogue,
+// output dtype, one 16- or 8-byte store when the row is aligned for it
+__device__ __forceinline__ void store_c4(const GemmArgs& p, int64_t row_off, int col, f32x4 v) {
+    const int n_left = p.N - col;
+    if (n_left <= 0) return;
+    if (p.ep_on) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int64_t idx = row_off + col + e;
+            if (e < n_left) v[e] = apply_epilogue(p.ep, v[e], idx, col + e);
+        }
+    }
+    const int64_t i = row_off + col;
+    if (p.vec_c && n_left >= 4) {
+        if (p.c_dtype == 0) {
+            *reinterpret_cast<f32x4*>((float*)p.C + i) = v;
+        } else {
+            u32x2 h;
+            if (p.c_dtype == 1) {
+                h[0] = f32_to_f16_bits(v[0]) | ((uint32_t)f32_to_f16_bits(v[1]) << 16);
+                h[1] = f32_to_f16_bits(v[2]) | ((uint32_t)f32_to_f16_bits(v[3]) << 16);
+            } else {
+                h[0] = f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
+                h[1] = f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16);
+            }
+            *reinterpret_cast<u32x2*>((uint16_t*)p.C + i) = h;
+        }
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        if (e < n_left) store_out(p.C, i + e, v[e], p.c_dtype);
+}
 
 template <bool BF16>
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
@@ -127,6 +187,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(const GemmArg
     constexpr int LA = (BM + BN) / G::RPI / NW;  // direct-load instructions per wave per stage
     constexpr int SLOT = (BM + BN) * ROWH;       // elements per ring slot
     static_assert(TM + TN <= 15, "fragment reads must fit the lgkmcnt field");
+    // the store pass reuses the ring: a 32 x 36 fp32 staging tile per wave
+    static_assert(STAGES * SLOT * 2 >= NW * 32 * 36 * 4, "ring too small for the store staging");
     __shared__ __attribute__((aligned(1024))) uint16_t smem[STAGES * SLOT];
 
     // Tile order: blocks are dealt round-robin to the 8 XCDs; give each XCD a
@@ -259,53 +321,85 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(const GemmArg
         }
     }
 
-    if (p.splits > 1) {   // fp32 partial for the reduce kernel
-        float* ws = p.ws + (int64_t)blockIdx.z * p.M * p.N;
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const int col = n0 + wn * WN + j * 32 + (lane & 31);
-                if (col >= p.N) continue;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    if (row < p.M) ws[(int64_t)row * p.N + col] = acc[i][j][r];
-                }
-            }
-        return;
-    }
     const int64_t c_off = (int64_t)batch * p.sC;
-    if (!p.ep_on) {
+    float* ws = p.splits > 1 ? p.ws + (int64_t)blockIdx.z * p.M * p.N : nullptr;
+    const bool vec = ws ? p.vec_ws : p.vec_c;
+    if (!vec) {   // rows off the vector grid: straight from the accumulators, 32 columns per row
+        if (ws) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const int col = n0 + wn * WN + j * 32 + (lane & 31);
-                if (col >= p.N) continue;
+                for (int j = 0; j < TN; ++j) {
+                    const int col = n0 + wn * WN + j * 32 + (lane & 31);
+                    if (col >= p.N) continue;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    if (row < p.M) store_out(p.C, c_off + (int64_t)row * p.ldc + col, acc[i][j][r], p.c_dtype);
-                }
-            }
-    } else {   // fused epilogue: the per-element code is larger, so only the tile loops unroll
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const int col = n0 + wn * WN + j * 32 + (lane & 31);
-                if (col >= p.N) continue;
-#pragma unroll 4
-                for (int r = 0; r < 16; ++r) {
-                    const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    if (row < p.M) {
-                        const int64_t idx = c_off + (int64_t)row * p.ldc + col;
-                        store_out(p.C, idx, apply_epilogue(p.ep, acc[i][j][r], idx, col), p.c_dtype);
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        if (row < p.M) ws[(int64_t)row * p.N + col] = acc[i][j][r];
                     }
                 }
-            }
+        } else if (!p.ep_on) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int col = n0 + wn * WN + j * 32 + (lane & 31);
+                    if (col >= p.N) continue;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        if (row < p.M) store_out(p.C, c_off + (int64_t)row * p.ldc + col, acc[i][j][r], p.c_dtype);
+                    }
+                }
+        } else {   // fused epilogue: the per-element code is larger, so only the tile loops unroll
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int col = n0 + wn * WN + j * 32 + (lane & 31);
+                    if (col >= p.N) continue;
+#pragma unroll 4
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        if (row < p.M) {
+                            const int64_t idx = c_off + (int64_t)row * p.ldc + col;
+                            store_out(p.C, idx, apply_epilogue(p.ep, acc[i][j][r], idx, col), p.c_dtype);
+                        }
+                    }
+                }
+        }
+        return;
     }
+    // Aligned rows: through LDS.  Each wave writes one 32x32 accumulator tile
+    // at a time into its own region of the (now idle) ring, row-major with a
+    // 36-float pitch (rows r and r+4, written by lanes l and l+32, land 16
+    // banks apart), and reads it back as 4 consecutive columns per lane, 8 rows
+    // per pass: 16-byte global stores, and per-element code (epilogue, dtype)
+    // in a loop rather than unrolled over the 16 * TM * TN accumulators.
+    __syncthreads();   // every wave is done with the ring (all its loads have landed)
+    constexpr int CS = 36;
+    float* cst = reinterpret_cast<float*>(smem) + wave * 32 * CS;
+    const int srow = lane >> 3, scol = (lane & 7) * 4;
+    // (compile-time tile indices: a rolled tile loop would index acc at run time
+    // and move it to scratch memory)
+    static_for<TM * TN>([&](auto IJ) {
+        constexpr int i = decltype(IJ)::value / TN, j = decltype(IJ)::value % TN;
+        {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                cst[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * CS + (lane & 31)] = acc[i][j][r];
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's writes, before its reads
+            const int row0 = m0 + wm * WM + i * 32, col = n0 + wn * WN + j * 32 + scol;
+            for (int t = 0; t < 4; ++t) {
+                const int row = row0 + srow + 8 * t;
+                const f32x4 v = *reinterpret_cast<const f32x4*>(cst + (srow + 8 * t) * CS + scol);
+                if (row >= p.M) continue;
+                if (ws) store_partial4(ws, (int64_t)row * p.N + col, v, p.N - col);
+                else store_c4(p, c_off + (int64_t)row * p.ldc, col, v);
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // reads done before the next tile's writes
+        }
+    });
 }
 
 // Sums the split-K partials in split order (deterministic), applies the
@@ -503,6 +597,11 @@ hipError_t launch_gemm_mfma(hipStream_t s, const void* A, int ab_dtype, const vo
     a.splits = g.splits;
     a.split_stages = g.split_stages;
     a.ws = (float*)workspace;
+    {
+        const int es = c_dtype == MVLM_F32 ? 4 : 2;
+        a.vec_c = ((uintptr_t)C % (4 * es) == 0) && (ldc % 4 == 0) && (strideC % 4 == 0);
+        a.vec_ws = N % 4 == 0;
+    }
     const int n = (int)w.pad_a + (int)w.pad_b + 1 + (g.splits > 1 ? 1 : 0);
     int idx = 0;
     if (w.pad_a) {

@@ -139,6 +139,8 @@ _SIGNATURES = {
     "mvlm_plan_add_gemm_batched": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int,
                                            c_int64, c_int64, c_int64, c_int64, c_int64, c_int64]),
     "mvlm_plan_use_graph": (c_int, [_P, c_int]),
+    "mvlm_plan_set_persistent": (c_int, [_P, c_int]),
+    "mvlm_plan_status": (c_int, [_P]),
     "mvlm_plan_run": (c_int, [_P, c_int, _PP]),
     "mvlm_plan_profile": (c_int, [_P, POINTER(c_float), c_int]),
     "mvlm_marker_record": (c_int, [_P, _PP]),
@@ -414,6 +416,15 @@ class Plan:
         _call("mvlm_plan_create", dev.handle, byref(h))
         self.handle = h
         self._keep = []
+
+    def set_persistent(self, enable=True):
+        """serve runs of consecutive M = 1 Q8_0 / Q4_0 GEMV entries with one persistent launch each"""
+        _call("mvlm_plan_set_persistent", self.handle, 1 if enable else 0)
+        return self
+
+    def status(self):
+        """wait for the plan's work; raises if a persistent launch gave up"""
+        _call("mvlm_plan_status", self.handle)
 
     def __len__(self):
         return lib().mvlm_plan_size(self.handle)
