@@ -381,12 +381,13 @@ def gemm_bench_matrix(dev, m, warmup=5, iters=20):
         for v in GEMM_BENCH_VARIANTS:
             if v.startswith("gemv") and M != 1:
                 continue
+            run = launch[v]
             for _ in range(warmup):
-                launch(False)
+                run(False)
             dev.sync()
             ts = []
             for _ in range(iters):
-                ev = launch(True)
+                ev = run(True)
                 ev.wait()
                 ts.append(ev.elapsed_ms())
             avg = float(np.mean(ts))
