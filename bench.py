@@ -648,9 +648,10 @@ def pmc_summarize(fetch_dir, write_dir, out=TRAFFIC_FILE):
                "hbm_bytes_per_step": total, "ratio_to_algorithmic": total / alg, "fetch": res["fetch"],
                "write": res["write"],
                "command": "cd /tmp && export TMPDIR=/tmp && rocprofv3 --pmc FETCH_SIZE -d $OUT/pmc_fetch "
-                          "-o run --output-format csv -- python3 $R/bench.py --pmc-probe; same with WRITE_SIZE "
-                          "into $OUT/pmc_write; python3 $R/bench.py --pmc-summarize $OUT/pmc_fetch "
-                          "$OUT/pmc_write   (R = repository root, OUT = an output directory)"}
+                          "-o run --output-format csv -- python3 $R/bench.py --pmc-workload decode_q8_0_m1; same "
+                          "with WRITE_SIZE into $OUT/pmc_write; python3 $R/bench.py --pmc-summarize "
+                          "$OUT/pmc_fetch $OUT/pmc_write   (R = repository root, OUT = an output directory; "
+                          "--pmc-probe in place of --pmc-workload decode_q8_0_m1 gives the same step)"}
     with open(out, "w") as fh:
         json.dump(summary, fh, indent=1)
     print(json.dumps(summary, indent=1))
