@@ -141,20 +141,23 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
     wait_vmcnt<R * CW>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    // Q4_0, one row of x: the block sums of x (the -8 offset's term), once per
-    // workgroup into LDS after the scales, instead of once per chunk and wave
-    constexpr bool kSumX = std::is_same_v<F, Q4Fmt> && MX == 1;
+    // Q4_0: the block sums of each row of x (the -8 offset's term, sxl[m][b]),
+    // once per workgroup into LDS after the scales, instead of once per chunk,
+    // row and wave
+    constexpr bool kSumX = std::is_same_v<F, Q4Fmt>;
     const float* sxl = reinterpret_cast<const float*>(lds + x_region + ((P.rows_per_block * nb * 2 + 30 + 1023) & ~1023));
     if constexpr (kSumX) {
-        for (int b = threadIdx.x; b < nb; b += 64 * NWAVE) {
+        for (int t = threadIdx.x; t < MX * nb; t += 64 * NWAVE) {
+            const int m = MX == 1 ? 0 : t / nb, b = MX == 1 ? t : t - m * nb;
+            const u32x4* xm = reinterpret_cast<const u32x4*>(lds + m * x_stride);
             XRaw<XT, WPL> xr;
 #pragma unroll
             for (int v = 0; v < SL; ++v) {
-                const u32x4 u = reinterpret_cast<const u32x4*>(lds)[x_slot<SL>(SL * b + v)];
+                const u32x4 u = xm[x_slot<SL>(SL * b + v)];
                 xr.d[4 * v + 0] = u[0]; xr.d[4 * v + 1] = u[1];
                 xr.d[4 * v + 2] = u[2]; xr.d[4 * v + 3] = u[3];
             }
-            const_cast<float*>(sxl)[b] = x_block_sum(xr);
+            const_cast<float*>(sxl)[t] = x_block_sum(xr);
         }
         // LDS-only fences around the barrier: the code loads stay in flight
         // (a full __syncthreads() would wait for them)
@@ -211,12 +214,16 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
                 const u32x2 u = *reinterpret_cast<const u32x2*>(xl + xbyte);
                 xr.d[0] = u[0]; xr.d[1] = u[1];
             }
+            float sx = 0.0f;
+            if constexpr (kSumX) sx = sxl[m * nb + (kk[i] >> 5)];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 uint16_t dh = 0;
                 if constexpr (F::QUANT)
                     dh = *reinterpret_cast<const uint16_t*>(lds + x_region + srow[r] + (kk[i] >> 5) * 2);
-                const float v = chunk_dot(F{}, q[r][i], dh, xr, acc[r][m]);
+                float v;
+                if constexpr (kSumX) v = chunk_dot_q4(q[r][i], dh, xr, sx, acc[r][m]);
+                else v = chunk_dot(F{}, q[r][i], dh, xr, acc[r][m]);
                 acc[r][m] = valid[i] ? v : acc[r][m];
             }
         }
@@ -367,7 +374,7 @@ static size_t stream_lds_bytes(const mvlm_weight* w, int x_dtype, int shape, int
     size_t bytes = (size_t)mx * ((x_bytes + 1023) & ~(size_t)1023);
     if (is_quant(w->dtype))
         bytes += ((size_t)rows_per_block(shape) * (size_t)(w->K / 32) * 2 + 30 + 1023) & ~(size_t)1023;
-    if (w->dtype == MVLM_Q4_0 && mx == 1) bytes += (size_t)(w->K / 32) * 4;   // block sums of x
+    if (w->dtype == MVLM_Q4_0) bytes += (size_t)mx * (w->K / 32) * 4;   // block sums of each row of x
     return bytes;
 }
 
