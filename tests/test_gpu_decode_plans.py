@@ -57,7 +57,8 @@ def check_outputs(dev, orc, weights, io, M):
     return xs
 
 
-@pytest.mark.parametrize("qt,M", [("q8_0", 1), ("q4_0", 1), ("q4_0", 4), ("q8_0", 4), ("q4_0", 16)])
+@pytest.mark.parametrize("qt,M", [("q8_0", 1), ("q4_0", 1), ("q4_0", 2), ("q8_0", 3), ("q4_0", 4), ("q8_0", 4),
+                                  ("q8_0", 9), ("q4_0", 16), ("q8_0", 16)])
 def test_decode_step_plan_outputs(dev, orc, qt, M):
     print(f"[decode plan] {qt} M={M}", flush=True)
     plan, weights, grouped, io = bench.build_decode_plan(dev, m, qt, M, True)
