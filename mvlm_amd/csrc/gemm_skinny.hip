@@ -13,7 +13,10 @@
 //    24 significant bits, fp32's own precision, over fp32's exponent range;
 //  * bf16 x bf16 products are exact in fp32 and the MFMA accumulates in fp32;
 //  * the block scale d (fp16, exact in fp32) is applied once per block of 32
-//    weights: acc += d * (sum over the block), as in the M = 1 kernel.
+//    weights: acc += d * (sum over the block), as in the M = 1 kernel;
+//  * Q4_0 multiplies the raw nibbles c and subtracts 8 * (sum of x over the
+//    block), that sum coming from one more product of the split x with a
+//    ones operand, shared by the block's row groups.
 // One MFMA covers 16 weight rows x one block of 32 weights x 16 rows of X
 // (rows m >= M are zero).  Operand layout of v_mfma_f32_16x16x32_bf16: lane l
 // supplies A[l%16][8*(l/16) .. +7] and B[8*(l/16) .. +7][l%16]; accumulator
@@ -71,14 +74,25 @@ __device__ __forceinline__ void split3(const float (&x)[8], u32x4& p1, u32x4& p2
     }
 }
 
-// 8 small integers (exact in bf16) from 8 code bytes / nibbles
+// 8 small integers (exact in bf16) from 8 code bytes / nibbles.  Q4_0 gives
+// the raw nibbles c (0..15): masked into bytes, one byte-to-float conversion
+// each; the -8 of (c - 8) is applied per block through the block sums of x.
 template <bool Q4>
 __device__ __forceinline__ u32x4 codes_to_bf16(u32x2 raw, int q) {
     float v[8];
     if constexpr (Q4) {
         const int shift = (q >> 1) * 4;
+        uint32_t lo = (raw[0] >> shift) & 0x0F0F0F0Fu, hi = (raw[1] >> shift) & 0x0F0F0F0Fu;
+        // opaque to the compiler, which would otherwise fold each byte's
+        // shift and mask into a bit-field extract per code in front of the
+        // conversion; this way v_cvt_f32_ubyte{0..3} read the bytes directly
+        asm_pin(lo);
+        asm_pin(hi);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = (float)((int)((raw[j >> 2] >> (8 * (j & 3) + shift)) & 0xFu) - 8);
+        for (int j = 0; j < 4; ++j) {
+            v[j] = (float)((lo >> (8 * j)) & 0xFFu);
+            v[4 + j] = (float)((hi >> (8 * j)) & 0xFFu);
+        }
     } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = (float)(int8_t)(raw[j >> 2] >> (8 * (j & 3)));
@@ -205,7 +219,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(const SkinnyGroup 
         }
     };
 
-    const bool xrow_live = l16 < M;                   // this lane's X row (A row)
+    // Lanes whose X row is past M (clamped to row M - 1 above) only feed
+    // output rows m >= M, which are never stored.
     f32x4 acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -246,11 +261,18 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(const SkinnyGroup 
             float x[8];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                x[j] = xrow_live ? __uint_as_float(xr[g][0][j]) : 0.0f;
-                x[4 + j] = xrow_live ? __uint_as_float(xr[g][1][j]) : 0.0f;
+                x[j] = __uint_as_float(xr[g][0][j]);
+                x[4 + j] = __uint_as_float(xr[g][1][j]);
             }
             u32x4 p1, p2, p3;
             split3(x, p1, p2, p3);
+            f32x4 sx = {0.0f, 0.0f, 0.0f, 0.0f};      // Q4_0: sum of the block's x per X row
+            if constexpr (Q4) {
+                const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};   // bf16 1.0 pairs
+                sx = mfma16(p1, ones, sx);
+                sx = mfma16(p2, ones, sx);
+                sx = mfma16(p3, ones, sx);
+            }
 #pragma unroll
             for (int rr = 0; rr < R; ++rr) {
                 const u32x4 w = codes_to_bf16<Q4>(raw[g][rr], q);
@@ -258,6 +280,10 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(const SkinnyGroup 
                 c = mfma16(p1, w, c);
                 c = mfma16(p2, w, c);
                 c = mfma16(p3, w, c);
+                if constexpr (Q4) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) c[i] = __builtin_fmaf(-8.0f, sx[i], c[i]);
+                }
                 const float d = f16_bits_to_f32((uint16_t)dh[g][rr]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[rr][i] = __builtin_fmaf(d, c[i], acc[rr][i]);
