@@ -36,7 +36,9 @@
 // per instruction), double-buffered, and read back per lane (ds_read_b64).
 // The 16-byte pieces of each LDS row are XOR-swizzled with row bits so the
 // 16 lanes of a read hit distinct banks.  The block's scales (all K) are
-// staged once per block.  X goes straight to registers, one step ahead.
+// staged once per block.  X goes straight to registers, one step ahead:
+// each block's X registers are refilled for the next step as soon as that
+// block's products are issued.
 // The NW partial tiles meet in LDS.  Splitting K over blocks instead (to give
 // small-N problems more blocks) would need a cross-block combine; on MI355X a
 // device-scope release fence per block costs ~90 ns, serialized (1024 blocks:
@@ -150,7 +152,7 @@ struct SkinnyGroup {
 };
 
 template <bool Q4, int R, int NW>
-__global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(const SkinnyGroup g) {
+__global__ __launch_bounds__(64 * NW, 4) void gemm_skinny_kernel(const SkinnyGroup g) {
     using L = SkinnyLayout<Q4>;
     constexpr int ROWS = 16 * R;
     constexpr int SLOT = skinny_slot_bytes<Q4, R, NW>();
@@ -208,15 +210,11 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(const SkinnyGroup 
             __builtin_amdgcn_global_load_lds(codes + row * ld + off, (lds_void*)(slot + t * 1024), 16, 0, 0);
         }
     };
-    // X of one step into registers
-    auto load_x = [&](int step, u32x4 (&xr)[SK_G][2]) {
-        const int kb = b0 + step * SK_G;
-#pragma unroll
-        for (int g = 0; g < SK_G; ++g) {
-            const int bb = min(kb + g, nb - 1);
-            xr[g][0] = asm_global_load_b128(xrow + 32 * bb);
-            xr[g][1] = asm_global_load_b128(xrow + 32 * bb + 4);
-        }
+    // X of block g of one step into registers
+    auto load_x = [&](int step, int g, u32x4 (&xg)[2]) {
+        const int bb = min(b0 + step * SK_G + g, nb - 1);
+        xg[0] = asm_global_load_b128(xrow + 32 * bb);
+        xg[1] = asm_global_load_b128(xrow + 32 * bb + 4);
     };
 
     // Lanes whose X row is past M (clamped to row M - 1 above) only feed
@@ -224,14 +222,25 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(const SkinnyGroup 
     f32x4 acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    if (steps > 0) issue_codes(0, 0);
+    u32x4 xr[SK_G][2];                                // X of the current step
+    if (steps > 0) {
+        issue_codes(0, 0);
+#pragma unroll
+        for (int g = 0; g < SK_G; ++g) load_x(0, g, xr[g]);
+    }
     asm_wait_vmcnt<0>();
     __syncthreads();                                  // the staged scales of every wave
 
     // LDS reads go through inline asm (the compiler would otherwise wait for
     // every in-flight direct load, including the next step's, before them)
     const uint32_t lds_base = lds_offset(lds);
-    auto compute = [&](int step, const u32x4 (&xr)[SK_G][2]) {
+    // Block g's X registers are refilled with the next step's X as soon as
+    // its products are issued, so those loads overlap this step's work.  The
+    // body is straight-line code (blocks past the wave's range get a zero
+    // scale, the refill is unconditional and clamped in bounds): with no
+    // branches the loop-carried X registers need no copies, which would read
+    // them while their loads are still in flight.
+    auto compute = [&](int step, u32x4 (&xr)[SK_G][2], auto refill) {
         const int kb = b0 + step * SK_G;
         const uint32_t slot = lds_offset(slots + (step & 1) * SLOT);
         u32x2 raw[SK_G][R];
@@ -257,7 +266,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(const SkinnyGroup 
             }
 #pragma unroll
         for (int g = 0; g < SK_G; ++g) {
-            if (kb + g >= b1) continue;               // uniform over the wave
+            const bool live = kb + g < b1;            // uniform over the wave
             float x[8];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -284,29 +293,37 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(const SkinnyGroup 
 #pragma unroll
                     for (int i = 0; i < 4; ++i) c[i] = __builtin_fmaf(-8.0f, sx[i], c[i]);
                 }
-                const float d = f16_bits_to_f32((uint16_t)dh[g][rr]);
+                const float d = live ? f16_bits_to_f32((uint16_t)dh[g][rr]) : 0.0f;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[rr][i] = __builtin_fmaf(d, c[i], acc[rr][i]);
             }
+            if constexpr (decltype(refill)::value) load_x(step + 1, g, xr[g]);
         }
     };
 
-    // Per step: X loads (L2-resident, consumed in the same iteration), then the
-    // next step's codes (the last step re-reads its own codes into the idle
-    // slot, which keeps the count uniform); waiting until only those remain in
-    // flight covers this step's X and codes.  X also goes through untracked
-    // loads, so the compiler adds no waits of its own in the loop.
-    for (int step = 0; step < steps; ++step) {
-        u32x4 xr[SK_G][2];
-        load_x(step, xr);
-        issue_codes(step + 1 < steps ? step + 1 : step, (step + 1) & 1);
+    // Per step: the next step's codes; waiting until only those remain in
+    // flight covers this step's X (requested during the previous step, or
+    // before the loop) and codes.  The last step is peeled: nothing is
+    // requested for it, and it waits for everything.  X goes through
+    // untracked loads, so the compiler adds no waits of its own.
+    for (int step = 0; step + 1 < steps; ++step) {
+        issue_codes(step + 1, (step + 1) & 1);
         asm_wait_vmcnt<NDMA>();
 #pragma unroll
         for (int g = 0; g < SK_G; ++g) {
             asm_pin(xr[g][0]);
             asm_pin(xr[g][1]);
         }
-        compute(step, xr);
+        compute(step, xr, std::true_type{});
+    }
+    asm_wait_vmcnt<0>();
+    if (steps > 0) {
+#pragma unroll
+        for (int g = 0; g < SK_G; ++g) {
+            asm_pin(xr[g][0]);
+            asm_pin(xr[g][1]);
+        }
+        compute(steps - 1, xr, std::false_type{});
     }
 
     // combine the NW partial tiles (reusing the code slots)
