@@ -116,6 +116,58 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 
+// v of the lane that DPP control `ctrl` names (all lanes valid).
+template <int ctrl>
+__device__ __forceinline__ float dpp_get(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false));
+}
+
+// DPP control that reads, for every lane, a lane of the same 16-lane row whose
+// index differs in bit B and agrees in the bits below it: quad_perm [1,0,3,2],
+// quad_perm [2,3,0,1], row_ror:4, row_ror:8.  (The rotations are not pairings,
+// but lane i and the lane it reads still differ in bit B only among bits <= B.)
+template <int B>
+constexpr int kDppFlip = B == 0 ? 0xB1 : B == 1 ? 0x4E : B == 2 ? 0x124 : 0x128;
+
+template <int B, int N>
+__device__ __forceinline__ void wave_sum_lanes_step(float (&w)[N], int lane) {
+    if constexpr (B < 4) {
+        constexpr int cur = (N >> B) > 1 ? (N >> B) : 1;   // values still carried per lane
+        if constexpr (cur > 1) {
+            // halve: lanes with bit B set keep the odd entries, the others the
+            // even ones, and each adds the entry its DPP source does not keep
+            const bool up = (lane >> B) & 1;
+#pragma unroll
+            for (int k = 0; k < cur / 2; ++k) {
+                const float keep = up ? w[2 * k + 1] : w[2 * k];
+                const float give = up ? w[2 * k] : w[2 * k + 1];
+                w[k] = keep + dpp_get<kDppFlip<B>>(give);
+            }
+        } else {
+            w[0] += dpp_get<kDppFlip<B>>(w[0]);
+        }
+        wave_sum_lanes_step<B + 1, N>(w, lane);
+    }
+}
+
+// Sums each of v[0..N) over the 64 lanes of a wavefront (N = 1, 2, 4, 8, 16);
+// lane l receives the total of index l & (N - 1).  The values are halved
+// across lanes first (one DPP add per pair and step), so N sums cost about
+// 3N + 6 instructions instead of N full reductions, and the N totals end up
+// in N different lanes.  Row sums are combined with two lane shuffles.
+template <int N>
+__device__ __forceinline__ float wave_sum_lanes(const float (&v)[N], int lane) {
+    static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "power of two up to 16");
+    float w[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) w[i] = v[i];
+    wave_sum_lanes_step<0, N>(w, lane);
+    float t = w[0];
+    t += __shfl_xor(t, 16);
+    t += __shfl_xor(t, 32);
+    return t;
+}
+
 // LDS pointer type of the direct global->LDS loads (global_load_lds_*): lane i
 // of the instruction writes its bytes at base + i * width.
 typedef __attribute__((address_space(3))) void lds_void;

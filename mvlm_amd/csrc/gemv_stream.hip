@@ -228,12 +228,18 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
             }
         }
     }
+    // the R x MX sums over the wave: lane j < R * MX ends with sum j = r * MX + m
+    constexpr int NV = R * MX;
+    float flat[NV];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int m = 0; m < MX; ++m) acc[r][m] = wave_sum(acc[r][m]);
+        for (int m = 0; m < MX; ++m) flat[r * MX + m] = acc[r][m];
+    const float tot = wave_sum_lanes<NV>(flat, lane);
+    const int jr = (lane & (NV - 1)) / MX, jm = (lane & (NV - 1)) % MX;
 
-    // y[m][row] (and the epilogue's mul / residual [m][row], bias [row])
+    // y[m][row] (and the epilogue's mul / residual [m][row], bias [row]),
+    // the NV outputs of a wave stored by NV lanes at once
     auto store_row = [&](int row, int m, float v) {
         if constexpr (MX == 1) {
             store_out(P.y, row, P.ep_on ? apply_epilogue(P.ep, v, row, row) : v, P.y_dtype);
@@ -243,31 +249,15 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
         }
     };
     if constexpr (SPLIT == 1) {
-        if (lane == 0 && active) {
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int m = 0; m < MX; ++m)
-                    if (row0 + r < rb1 && (MX == 1 || m < P.M)) store_row(row0 + r, m, acc[r][m]);
-        }
+        if (lane < NV && active && row0 + jr < rb1 && (MX == 1 || jm < P.M)) store_row(row0 + jr, jm, tot);
     } else {
-        if (lane == 0) {
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int m = 0; m < MX; ++m) part[wave][r * MX + m] = acc[r][m];
-        }
+        if (lane < NV) part[wave][lane] = tot;
         __syncthreads();
-        if (wsub == 0 && lane == 0 && active) {
+        if (wsub == 0 && lane < NV && active) {
+            float v = part[wave][lane];
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int m = 0; m < MX; ++m) {
-                    float v = part[wave][r * MX + m];
-#pragma unroll
-                    for (int s = 1; s < SPLIT; ++s) v += part[wave + s][r * MX + m];
-                    if (row0 + r < rb1 && (MX == 1 || m < P.M)) store_row(row0 + r, m, v);
-                }
+            for (int s = 1; s < SPLIT; ++s) v += part[wave + s][lane];
+            if (row0 + jr < rb1 && (MX == 1 || jm < P.M)) store_row(row0 + jr, jm, v);
         }
     }
 }
