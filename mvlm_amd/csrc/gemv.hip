@@ -93,14 +93,10 @@ __global__ __launch_bounds__(256) void gemv_dense_kernel(const XT* __restrict__ 
             for (int e = 0; e < E; ++e) acc[r] = __builtin_fmaf(xv[e], w[e], acc[r]);
         }
     }
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-    if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (row0 + r < N)
-                store_out(y, row0 + r, ep.any() ? apply_epilogue(ep, acc[r], row0 + r, row0 + r) : acc[r], y_dtype);
-    }
+    // lane r < R ends with row r's sum and stores it
+    const float tot = wave_sum_lanes<R>(acc, lane);
+    const int row = row0 + (lane & (R - 1));
+    if (lane < R && row < N) store_out(y, row, ep.any() ? apply_epilogue(ep, tot, row, row) : tot, y_dtype);
 }
 
 // Rows per wave: enough waves to cover the 256 CUs several times over, and
