@@ -364,7 +364,7 @@ int mvlm_plan_use_graph(mvlm_plan* plan, int enable);
  * mvlm_plan_status reports.  Enabling builds device tables (allocates); a
  * plan recorded as a graph must be recorded again after this call.  Off by
  * default: on MI355X the Phi-1.5 decode step takes 497 us (Q8_0) / 475 us
- * (Q4_0) this way against 360 / 303 us as a graph of separate launches. */
+ * (Q4_0) this way against 359 / 294 us as a graph of separate launches. */
 int mvlm_plan_set_persistent(mvlm_plan* plan, int enable);
 /* Waits for the plan's stream and reports MVLM_ERR_HIP if a persistent launch
  * gave up (its outputs are then not valid). */
