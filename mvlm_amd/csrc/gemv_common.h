@@ -37,7 +37,9 @@ struct Q4Fmt {
     static constexpr int WPL = 32;
     static constexpr bool QUANT = true;
     static constexpr int MIN_WAVES = 4;                // 32 x values per lane need more registers
-    static constexpr int MIN_WAVES_BATCH = 2;          // and 4 rows of x 4x as many
+    // 4 rows of x: at most 128 VGPRs (a few prologue values spill), so two
+    // 8-wave blocks fit per CU; with 145 VGPRs only one did (M=4 step 568 -> 520 us)
+    static constexpr int MIN_WAVES_BATCH = 4;
 };
 
 // x values of one chunk as raw bits: E elements of XT in XD dwords.
