@@ -50,7 +50,7 @@ struct StreamProblem {
     void* y;                       // [M][N]
     int64_t ld_bytes;
     int N, K, y_dtype;
-    int M;                         // rows of x (1 for MX = 1; 1..4 for MX = 4)
+    int M;                         // rows of x (1 for MX = 1; 2 for MX = 2; 3..4 for MX = 4)
     int shape;                     // index into kShapes
     int rows_per_block;            // block j owns rows [j*rows_per_block, (j+1)*rows_per_block) below N
     int block_begin;               // first block of this problem in the grid
@@ -370,11 +370,16 @@ static size_t stream_lds_bytes(const mvlm_weight* w, int x_dtype, int shape, int
 
 constexpr size_t STREAM_LDS_MAX = 152 * 1024;
 
+// Rows of x a launch's kernel carries: M = 2 has its own kernel (two fmas per
+// converted weight), M = 3 and 4 share the four-row kernel (rows at or past M
+// repeat row M - 1 and are not stored).
+static int batch_mx(int M) { return M <= 1 ? 1 : M == 2 ? 2 : 4; }
+
 bool stream_supported(const mvlm_weight* w, int M) {
     const int shape = stream_shape(w, M, 0);
     if (M > 1 && (M > 4 || !is_quant(w->dtype))) return false;
     return shape >= 0 && w->K % weight_wpl(w->dtype) == 0 &&
-           stream_lds_bytes(w, MVLM_F32, shape, M > 1 ? 4 : 1) <= STREAM_LDS_MAX;
+           stream_lds_bytes(w, MVLM_F32, shape, batch_mx(M)) <= STREAM_LDS_MAX;
 }
 
 int stream_max_group() { return MAX_GROUP; }
@@ -446,11 +451,12 @@ hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const*
             p.ep_on = 1;
         }
         if (p.shape < 0 || w->dtype != dtype || (M > 1 && y_dtypes[i] != MVLM_F32)) return hipErrorInvalidValue;
-        const size_t b = stream_lds_bytes(w, x_dtype, p.shape, M > 1 ? 4 : 1);
+        const size_t b = stream_lds_bytes(w, x_dtype, p.shape, batch_mx(M));
         lds = b > lds ? b : lds;
     }
     if (lds > STREAM_LDS_MAX) return hipErrorInvalidValue;
-    if (M > 1) return dtype == MVLM_Q8_0 ? launch_group<Q8Fmt, float, 4>(s, g, lds) : launch_group<Q4Fmt, float, 4>(s, g, lds);
+    if (M == 2) return dtype == MVLM_Q8_0 ? launch_group<Q8Fmt, float, 2>(s, g, lds) : launch_group<Q4Fmt, float, 2>(s, g, lds);
+    if (M > 2) return dtype == MVLM_Q8_0 ? launch_group<Q8Fmt, float, 4>(s, g, lds) : launch_group<Q4Fmt, float, 4>(s, g, lds);
     switch (dtype) {
         case MVLM_Q8_0: return launch_group<Q8Fmt, float>(s, g, lds);
         case MVLM_Q4_0: return launch_group<Q4Fmt, float>(s, g, lds);
@@ -487,9 +493,14 @@ hipError_t launch_gemv_stream_batch(hipStream_t s, const float* x, const mvlm_we
         p.ep = *ep;
         p.ep_on = 1;
     }
-    const size_t lds = stream_lds_bytes(W, MVLM_F32, p.shape, 4);
-    if (W->dtype == MVLM_Q8_0) return launch_group<Q8Fmt, float, 4>(s, g, lds);
-    if (W->dtype == MVLM_Q4_0) return launch_group<Q4Fmt, float, 4>(s, g, lds);
+    const size_t lds = stream_lds_bytes(W, MVLM_F32, p.shape, batch_mx(M));
+    if (M == 2) {
+        if (W->dtype == MVLM_Q8_0) return launch_group<Q8Fmt, float, 2>(s, g, lds);
+        if (W->dtype == MVLM_Q4_0) return launch_group<Q4Fmt, float, 2>(s, g, lds);
+    } else {
+        if (W->dtype == MVLM_Q8_0) return launch_group<Q8Fmt, float, 4>(s, g, lds);
+        if (W->dtype == MVLM_Q4_0) return launch_group<Q4Fmt, float, 4>(s, g, lds);
+    }
     return hipErrorInvalidValue;
 }
 
