@@ -27,11 +27,12 @@
 // j and j + 16).
 //
 // A block of NW waves owns R groups of 16 weight rows; wave w takes the w-th
-// NW-th of the K blocks and walks it in steps of G = 4 blocks.  Codes do not
-// go straight to registers: in the MFMA layout a wave instruction would touch
-// 16 rows x 32 bytes (16 partly used lines), and such loads ran at a fraction
-// of HBM speed whatever the arithmetic.  Instead each step's codes of the
-// wave's rows (16R rows x 128 bytes for Q8_0, x 64 bytes for Q4_0) are copied
+// NW-th of the K blocks and walks it in steps of G blocks (4, or 2 with four
+// row groups).  Codes do not go straight to registers: in the MFMA layout a
+// wave instruction would touch 16 rows x 32 bytes (16 partly used lines), and
+// such loads ran at a fraction of HBM speed whatever the arithmetic.  Instead
+// each step's codes of the wave's rows (16R rows x 32G bytes for Q8_0, x 16G
+// bytes for Q4_0) are copied
 // into the wave's own LDS slot with direct 16-byte loads (1 KiB contiguous
 // per instruction), double-buffered, and read back per lane (ds_read_b64).
 // The 16-byte pieces of each LDS row are XOR-swizzled with row bits so the
@@ -110,27 +111,30 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
                                                    0, 0, 0);
 }
 
-constexpr int SK_G = 4;          // K blocks per step
 constexpr size_t SKINNY_LDS_MAX = 160 * 1024;
 
-template <bool Q4>
+// G = K blocks per step.
+template <bool Q4, int G>
 struct SkinnyLayout {
     static constexpr int BB = Q4 ? 16 : 32;           // code bytes per block per row
-    static constexpr int CB = SK_G * BB;              // code bytes per row per step (64 / 128)
+    static constexpr int CB = G * BB;                 // code bytes per row per step (32 / 64 / 128)
     static constexpr int P = CB / 16;                 // 16-byte pieces per row per step
     static constexpr int RPI = 64 / P;                // rows per direct-load instruction
-    // physical piece of logical piece p in LDS row r
-    __device__ static int piece(int p, int r) { return p ^ (Q4 ? ((r >> 2) & 3) : ((r >> 1) & 7)); }
+    static constexpr int RSH = CB == 128 ? 1 : CB == 64 ? 2 : 3;   // 1 << RSH rows per 256 bytes
+    static_assert(CB == 32 || CB == 64 || CB == 128, "step rows of 32, 64 or 128 bytes");
+    // physical piece of logical piece p in LDS row r: the 16 rows of a read
+    // land on distinct banks
+    __device__ static int piece(int p, int r) { return p ^ ((r >> RSH) & (P - 1)); }
 };
 
 // LDS bytes of a block: the scales of its rows (all K), then two code slots
 // per wave; the partial tiles of the final combine reuse the slots.
-template <bool Q4, int R, int NW>
-__host__ __device__ constexpr int skinny_slot_bytes() { return 16 * R * SkinnyLayout<Q4>::CB; }
-template <bool Q4, int R, int NW>
+template <bool Q4, int R, int NW, int G>
+__host__ __device__ constexpr int skinny_slot_bytes() { return 16 * R * SkinnyLayout<Q4, G>::CB; }
+template <bool Q4, int R, int NW, int G>
 static size_t skinny_lds_bytes(int K) {
     const size_t scale_region = ((size_t)16 * R * (K / 32) * 2 + 255) / 256 * 256;
-    return scale_region + (size_t)NW * 2 * skinny_slot_bytes<Q4, R, NW>();
+    return scale_region + (size_t)NW * 2 * skinny_slot_bytes<Q4, R, NW, G>();
 }
 
 // One problem of a (possibly grouped) launch: Y[M][N] = X[M][K] w^T.
@@ -151,13 +155,14 @@ struct SkinnyGroup {
     int count, M;
 };
 
-template <bool Q4, int R, int NW>
+template <bool Q4, int R, int NW, int G>
 __global__ __launch_bounds__(64 * NW, 4) void gemm_skinny_kernel(const SkinnyGroup g) {
-    using L = SkinnyLayout<Q4>;
+    using L = SkinnyLayout<Q4, G>;
     constexpr int ROWS = 16 * R;
-    constexpr int SLOT = skinny_slot_bytes<Q4, R, NW>();
+    constexpr int SLOT = skinny_slot_bytes<Q4, R, NW, G>();
     constexpr int NDMA = ROWS / L::RPI;               // direct loads per step
     static_assert(NDMA <= 63, "direct loads of one step must fit vmcnt");
+    static_assert(2 * SLOT >= R * 1024, "the partial tiles of the combine must fit the code slots");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
     int pi = 0;                                       // blocks are dealt to the problems in order
@@ -178,7 +183,7 @@ __global__ __launch_bounds__(64 * NW, 4) void gemm_skinny_kernel(const SkinnyGro
     const int nb = K >> 5;
     const int per = (nb + NW - 1) / NW;
     const int b0 = wave * per, b1 = min(b0 + per, nb);
-    const int steps = b1 > b0 ? (b1 - b0 + SK_G - 1) / SK_G : 0;
+    const int steps = b1 > b0 ? (b1 - b0 + G - 1) / G : 0;
     const int64_t row_bytes = (int64_t)nb * L::BB;
 
     // scales of rows n0 .. n0+ROWS-1 (contiguous in the scale array) with
@@ -200,7 +205,7 @@ __global__ __launch_bounds__(64 * NW, 4) void gemm_skinny_kernel(const SkinnyGro
     const float* xrow = X + (int64_t)min(l16, M - 1) * K + 8 * q;
     const int dma_row = lane / L::P, dma_piece = lane % L::P;
     auto issue_codes = [&](int step, int slot_idx) {
-        const int kb = b0 + step * SK_G;
+        const int kb = b0 + step * G;
         uint8_t* slot = slots + slot_idx * SLOT;
 #pragma unroll
         for (int t = 0; t < NDMA; ++t) {
@@ -212,7 +217,7 @@ __global__ __launch_bounds__(64 * NW, 4) void gemm_skinny_kernel(const SkinnyGro
     };
     // X of block g of one step into registers
     auto load_x = [&](int step, int g, u32x4 (&xg)[2]) {
-        const int bb = min(b0 + step * SK_G + g, nb - 1);
+        const int bb = min(b0 + step * G + g, nb - 1);
         xg[0] = asm_global_load_b128(xrow + 32 * bb);
         xg[1] = asm_global_load_b128(xrow + 32 * bb + 4);
     };
@@ -222,11 +227,11 @@ __global__ __launch_bounds__(64 * NW, 4) void gemm_skinny_kernel(const SkinnyGro
     f32x4 acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    u32x4 xr[SK_G][2];                                // X of the current step
+    u32x4 xr[G][2];                                   // X of the current step
     if (steps > 0) {
         issue_codes(0, 0);
 #pragma unroll
-        for (int g = 0; g < SK_G; ++g) load_x(0, g, xr[g]);
+        for (int g = 0; g < G; ++g) load_x(0, g, xr[g]);
     }
     asm_wait_vmcnt<0>();
     __syncthreads();                                  // the staged scales of every wave
@@ -240,13 +245,13 @@ __global__ __launch_bounds__(64 * NW, 4) void gemm_skinny_kernel(const SkinnyGro
     // scale, the refill is unconditional and clamped in bounds): with no
     // branches the loop-carried X registers need no copies, which would read
     // them while their loads are still in flight.
-    auto compute = [&](int step, u32x4 (&xr)[SK_G][2], auto refill) {
-        const int kb = b0 + step * SK_G;
+    auto compute = [&](int step, u32x4 (&xr)[G][2], auto refill) {
+        const int kb = b0 + step * G;
         const uint32_t slot = lds_offset(slots + (step & 1) * SLOT);
-        u32x2 raw[SK_G][R];
-        uint32_t dh[SK_G][R];
+        u32x2 raw[G][R];
+        uint32_t dh[G][R];
 #pragma unroll
-        for (int g = 0; g < SK_G; ++g) {
+        for (int g = 0; g < G; ++g) {
             const int lpiece = Q4 ? g : 2 * g + (q >> 1);
             const int bb = min(kb + g, b1 - 1);
 #pragma unroll
@@ -258,14 +263,14 @@ __global__ __launch_bounds__(64 * NW, 4) void gemm_skinny_kernel(const SkinnyGro
         }
         asm_wait_lgkmcnt<0>();
 #pragma unroll
-        for (int g = 0; g < SK_G; ++g)
+        for (int g = 0; g < G; ++g)
 #pragma unroll
             for (int rr = 0; rr < R; ++rr) {
                 asm_pin(raw[g][rr]);
                 asm_pin(dh[g][rr]);
             }
 #pragma unroll
-        for (int g = 0; g < SK_G; ++g) {
+        for (int g = 0; g < G; ++g) {
             const bool live = kb + g < b1;            // uniform over the wave
             float x[8];
 #pragma unroll
@@ -310,7 +315,7 @@ __global__ __launch_bounds__(64 * NW, 4) void gemm_skinny_kernel(const SkinnyGro
         issue_codes(step + 1, (step + 1) & 1);
         asm_wait_vmcnt<NDMA>();
 #pragma unroll
-        for (int g = 0; g < SK_G; ++g) {
+        for (int g = 0; g < G; ++g) {
             asm_pin(xr[g][0]);
             asm_pin(xr[g][1]);
         }
@@ -319,7 +324,7 @@ __global__ __launch_bounds__(64 * NW, 4) void gemm_skinny_kernel(const SkinnyGro
     asm_wait_vmcnt<0>();
     if (steps > 0) {
 #pragma unroll
-        for (int g = 0; g < SK_G; ++g) {
+        for (int g = 0; g < G; ++g) {
             asm_pin(xr[g][0]);
             asm_pin(xr[g][1]);
         }
@@ -355,11 +360,22 @@ __global__ __launch_bounds__(64 * NW, 4) void gemm_skinny_kernel(const SkinnyGro
     }
 }
 
-// Tile shape of a launch by its total 16-row groups: two row groups per
-// block when that still gives every CU a block; fewer row groups than CUs get
-// 16-wave blocks (more loads in flight per block).
-enum SkinnyShape { SK_R2_W8, SK_R1_W8, SK_R1_W16 };
-static SkinnyShape skinny_shape(int64_t groups, int num_cus) {
+// Tile shape of a launch by its total 16-row groups.  Every wave reads its X
+// slice from L2 for each K block (2 KiB per block at M = 16, 4x the Q4_0 code
+// bytes of two row groups), so more row groups per wave means less X traffic
+// per weight.  Q4_0 takes four row groups per wave (16-wave blocks, two K
+// blocks per step, one block per CU) when those blocks fill the CUs in one
+// round (Phi-1.5 QKV+fc1, 896 row groups: M = 16 14.5 -> 12.9 us, M = 8
+// 12.7 -> 12.0 us); past one round the two-block-per-CU shape overlaps one
+// block's prologue with the other's loop and wins (LM head, 3200 row groups:
+// 41.0 us against 45.6 us).  Q8_0's codes are twice the bytes per weight, X
+// weighs half as much, and the shorter per-block chain lost (M = 8 QKV+fc1
+// 12.5 -> 13.5 us).  Then two row groups per block when that still gives
+// every CU a block; fewer row groups than CUs get 16-wave blocks (more loads
+// in flight per block).
+enum SkinnyShape { SK_R4_W16, SK_R2_W8, SK_R1_W8, SK_R1_W16 };
+static SkinnyShape skinny_shape(int64_t groups, int num_cus, bool q4) {
+    if (q4 && groups >= 3 * (int64_t)num_cus && groups <= 4 * (int64_t)num_cus) return SK_R4_W16;
     if (groups >= 2 * (int64_t)num_cus) return SK_R2_W8;
     if (groups >= num_cus) return SK_R1_W8;
     return SK_R1_W16;
@@ -368,9 +384,12 @@ static SkinnyShape skinny_shape(int64_t groups, int num_cus) {
 template <bool Q4>
 static size_t skinny_lds_for(SkinnyShape sh, int K) {
     switch (sh) {
-        case SK_R2_W8: return skinny_lds_bytes<Q4, 2, 8>(K);
-        case SK_R1_W8: return skinny_lds_bytes<Q4, 1, 8>(K);
-        default: return skinny_lds_bytes<Q4, 1, 16>(K);
+        case SK_R4_W16:
+            if constexpr (Q4) return skinny_lds_bytes<Q4, 4, 16, 2>(K);
+            return SKINNY_LDS_MAX + 1;                // Q4_0 only
+        case SK_R2_W8: return skinny_lds_bytes<Q4, 2, 8, 4>(K);
+        case SK_R1_W8: return skinny_lds_bytes<Q4, 1, 8, 4>(K);
+        default: return skinny_lds_bytes<Q4, 1, 16, 4>(K);
     }
 }
 
@@ -378,7 +397,7 @@ bool skinny_supported(int count, const mvlm_weight* const* ws, int num_cus) {
     if (num_cus <= 0) num_cus = 256;
     int64_t groups = 0;
     for (int i = 0; i < count; ++i) groups += (ws[i]->N + 15) / 16;
-    const SkinnyShape sh = skinny_shape(groups, num_cus);
+    const SkinnyShape sh = skinny_shape(groups, num_cus, count > 0 && ws[0]->dtype == MVLM_Q4_0);
     for (int i = 0; i < count; ++i) {
         const mvlm_weight* w = ws[i];
         if (!is_quant(w->dtype) || w->K % 32 != 0) return false;
@@ -388,17 +407,17 @@ bool skinny_supported(int count, const mvlm_weight* const* ws, int num_cus) {
     return true;
 }
 
-template <bool Q4, int R, int NW>
+template <bool Q4, int R, int NW, int G>
 static hipError_t launch_skinny(hipStream_t s, SkinnyGroup& g) {
-    auto kernel = gemm_skinny_kernel<Q4, R, NW>;
+    auto kernel = gemm_skinny_kernel<Q4, R, NW, G>;
     size_t lds = 0;
     unsigned blocks = 0;
     for (int i = 0; i < g.count; ++i) {
-        lds = std::max(lds, skinny_lds_bytes<Q4, R, NW>(g.p[i].K));
+        lds = std::max(lds, skinny_lds_bytes<Q4, R, NW, G>(g.p[i].K));
         g.p[i].block_begin = (int)blocks;
         blocks += (unsigned)((g.p[i].N + 16 * R - 1) / (16 * R));
     }
-    if (const hipError_t e = allow_dynamic_lds<gemm_skinny_kernel<Q4, R, NW>>((int)SKINNY_LDS_MAX); e != hipSuccess)
+    if (const hipError_t e = allow_dynamic_lds<gemm_skinny_kernel<Q4, R, NW, G>>((int)SKINNY_LDS_MAX); e != hipSuccess)
         return e;
     if (lds > SKINNY_LDS_MAX) return hipErrorInvalidValue;
     launch_kernel(kernel, dim3(blocks), dim3(64 * NW), (uint32_t)lds, s, g);
@@ -410,10 +429,13 @@ template <bool Q4>
 static hipError_t launch_skinny_shape(hipStream_t s, SkinnyGroup& g, int num_cus) {
     int64_t groups = 0;
     for (int i = 0; i < g.count; ++i) groups += (g.p[i].N + 15) / 16;
-    switch (skinny_shape(groups, num_cus)) {
-        case SK_R2_W8: return launch_skinny<Q4, 2, 8>(s, g);
-        case SK_R1_W8: return launch_skinny<Q4, 1, 8>(s, g);
-        default: return launch_skinny<Q4, 1, 16>(s, g);
+    switch (skinny_shape(groups, num_cus, Q4)) {
+        case SK_R4_W16:
+            if constexpr (Q4) return launch_skinny<Q4, 4, 16, 2>(s, g);
+            return hipErrorInvalidValue;              // Q4_0 only
+        case SK_R2_W8: return launch_skinny<Q4, 2, 8, 4>(s, g);
+        case SK_R1_W8: return launch_skinny<Q4, 1, 8, 4>(s, g);
+        default: return launch_skinny<Q4, 1, 16, 4>(s, g);
     }
 }
 

@@ -270,12 +270,14 @@ def test_quant_skinny_gemm(dev, orc, qt, M):
 @pytest.mark.parametrize("qt", [Q8, Q4])
 @pytest.mark.parametrize("M,N,K,xscale", [(4, 33, 32, 1.0), (16, 17, 96, 1.0), (3, 130, 8192, 1.0),
                                           (16, 6144, 2048, 1.0), (7, 300, 2048, 3.0e4), (9, 64, 1024, 1.0e-6),
-                                          (2, 51, 23 * 32, 1.0), (5, 8200, 96, 1.0), (16, 16400, 64, 1.0)])
+                                          (2, 51, 23 * 32, 1.0), (5, 8200, 96, 1.0), (16, 16400, 64, 1.0),
+                                          (16, 12300, 2048, 1.0), (6, 16384, 64, 1.0), (11, 13000, 8192, 1.0)])
 def test_quant_skinny_shapes(dev, orc, qt, M, N, K, xscale):
     # ragged N (not a multiple of the 16-row MFMA tile), fewer K blocks than
     # waves, long rows, x far from unit scale (the bf16 three-way split of x
     # must keep fp32 precision over fp32's range), and N large enough for the
-    # blocks with 2 and 4 row groups (ragged in the last block)
+    # blocks with 2 and 4 row groups per wave (ragged in the last block; 769
+    # to 1024 row groups take the four-group shape with its two-block steps)
     X = (orc.normal_f32(M * K, 171) * np.float32(xscale)).astype(np.float32)
     blocks = make_quant(orc, qt, N, K, 172)
     kind = "q8_0" if qt == Q8 else "q4_0"
@@ -575,6 +577,27 @@ def test_gemm_quant_grouped(dev, orc, qt, M):
         ref = orc.gemm_nk(kind, X.ravel(), b, M, N, K)
         _, S = orc.gemm_f64(X.astype(np.float64), deq(b).astype(np.float64).reshape(N, K), M, N, K)
         ok, worst = within(got, ref.reshape(M, N), S.reshape(M, N), 1e-5)
+        assert ok, (M, N, K, worst)
+
+
+@pytest.mark.parametrize("qt", [Q8, Q4])
+@pytest.mark.parametrize("M", [9, 16])
+def test_gemm_quant_grouped_phi_qkv_fc1(dev, orc, qt, M):
+    """the QKV + fc1 group of a Phi-1.5 block at full size (6144 + 8192 rows
+    over one x, 896 row groups): the skinny kernel's four-row-group shape"""
+    shapes = [(6144, 2048), (8192, 2048)]
+    kind = "q8_0" if qt == Q8 else "q4_0"
+    deq = orc.dequant_q8_0 if qt == Q8 else orc.dequant_q4_0
+    xh = orc.normal_f32(M * 2048, 301)
+    x = dev.upload(xh)
+    blocks = [make_quant(orc, qt, N, K, 302 + i) for i, (N, K) in enumerate(shapes)]
+    Ws = [dev.pack(b, qt, N, K) for b, (N, K) in zip(blocks, shapes)]
+    Ys = [dev.alloc(M * N * 4) for N, _ in shapes]
+    dev.gemm_quant_grouped(M, [(x, F32, W, y, F32) for W, y in zip(Ws, Ys)])
+    for (N, K), b, y in zip(shapes, blocks, Ys):
+        ref = orc.gemm_nk(kind, xh, b, M, N, K)
+        _, S = orc.gemm_f64(xh.astype(np.float64).reshape(M, K), deq(b).astype(np.float64).reshape(N, K), M, N, K)
+        ok, worst = within(y.download(np.float32).reshape(M, N), ref.reshape(M, N), S.reshape(M, N), 1e-5)
         assert ok, (M, N, K, worst)
 
 
