@@ -155,7 +155,8 @@ struct SkinnyGroup {
     int count, M;
 };
 
-template <bool Q4, int R, int NW, int G>
+// XS: odd rows read their X halves in swapped order (M > 8, below).
+template <bool Q4, int R, int NW, int G, bool XS>
 __global__ __launch_bounds__(64 * NW, 4) void gemm_skinny_kernel(const SkinnyGroup g) {
     using L = SkinnyLayout<Q4, G>;
     constexpr int ROWS = 16 * R;
@@ -215,11 +216,21 @@ __global__ __launch_bounds__(64 * NW, 4) void gemm_skinny_kernel(const SkinnyGro
             __builtin_amdgcn_global_load_lds(codes + row * ld + off, (lds_void*)(slot + t * 1024), 16, 0, 0);
         }
     };
-    // X of block g of one step into registers
+    // X of block g of one step into registers.  A lane's 8 floats are two
+    // 16-byte halves of its row's 128-byte line.  With XS, lanes of odd rows
+    // load the second half first, so the 16 lanes of a quarter-wave (16 rows,
+    // one q) read two different offsets of their lines instead of one (the
+    // vector cache serves many lines at one offset one after another: the
+    // Q4_0 M = 16 step 827 -> 766 us, Q8_0 M = 16 895 -> 783 us, Q8_0 M = 12
+    // 797 -> 760 us).  The halves are swapped back where the block is split;
+    // at M <= 8 (at most 8 distinct lines) those selects cost more than the
+    // conflicts (Q4_0 M = 5 707 -> 725 us), so XS is off there.
+    const bool xodd = XS && (min(l16, M - 1) & 1) != 0;   // parity of the row actually read
+    const int xsw = xodd ? 4 : 0;
     auto load_x = [&](int step, int g, u32x4 (&xg)[2]) {
         const int bb = min(b0 + step * G + g, nb - 1);
-        xg[0] = asm_global_load_b128(xrow + 32 * bb);
-        xg[1] = asm_global_load_b128(xrow + 32 * bb + 4);
+        xg[0] = asm_global_load_b128(xrow + 32 * bb + xsw);
+        xg[1] = asm_global_load_b128(xrow + 32 * bb + 4 - xsw);
     };
 
     // Lanes whose X row is past M (clamped to row M - 1 above) only feed
@@ -275,8 +286,8 @@ __global__ __launch_bounds__(64 * NW, 4) void gemm_skinny_kernel(const SkinnyGro
             float x[8];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                x[j] = __uint_as_float(xr[g][0][j]);
-                x[4 + j] = __uint_as_float(xr[g][1][j]);
+                x[j] = __uint_as_float(xodd ? xr[g][1][j] : xr[g][0][j]);
+                x[4 + j] = __uint_as_float(xodd ? xr[g][0][j] : xr[g][1][j]);
             }
             u32x4 p1, p2, p3;
             split3(x, p1, p2, p3);
@@ -409,7 +420,8 @@ bool skinny_supported(int count, const mvlm_weight* const* ws, int num_cus) {
 
 template <bool Q4, int R, int NW, int G>
 static hipError_t launch_skinny(hipStream_t s, SkinnyGroup& g) {
-    auto kernel = gemm_skinny_kernel<Q4, R, NW, G>;
+    const bool xs = g.M > 8;
+    auto kernel = xs ? gemm_skinny_kernel<Q4, R, NW, G, true> : gemm_skinny_kernel<Q4, R, NW, G, false>;
     size_t lds = 0;
     unsigned blocks = 0;
     for (int i = 0; i < g.count; ++i) {
@@ -417,7 +429,9 @@ static hipError_t launch_skinny(hipStream_t s, SkinnyGroup& g) {
         g.p[i].block_begin = (int)blocks;
         blocks += (unsigned)((g.p[i].N + 16 * R - 1) / (16 * R));
     }
-    if (const hipError_t e = allow_dynamic_lds<gemm_skinny_kernel<Q4, R, NW, G>>((int)SKINNY_LDS_MAX); e != hipSuccess)
+    if (const hipError_t e = xs ? allow_dynamic_lds<gemm_skinny_kernel<Q4, R, NW, G, true>>((int)SKINNY_LDS_MAX)
+                                : allow_dynamic_lds<gemm_skinny_kernel<Q4, R, NW, G, false>>((int)SKINNY_LDS_MAX);
+        e != hipSuccess)
         return e;
     if (lds > SKINNY_LDS_MAX) return hipErrorInvalidValue;
     launch_kernel(kernel, dim3(blocks), dim3(64 * NW), (uint32_t)lds, s, g);
