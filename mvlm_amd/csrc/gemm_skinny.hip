@@ -383,12 +383,15 @@ __global__ __launch_bounds__(64 * NW, 4) void gemm_skinny_kernel(const SkinnyGro
 // weighs half as much, and the shorter per-block chain lost (M = 8 QKV+fc1
 // 12.5 -> 13.5 us).  Then two row groups per block when that still gives
 // every CU a block; fewer row groups than CUs get 16-wave blocks (more loads
-// in flight per block).
+// in flight per block), and so do Q4_0 launches of one to two row groups per
+// CU (Phi-1.5 dense+fc2, 256 row groups: half the K steps per wave; Q4_0
+// steps M = 5 708 -> 688 us, M = 8 728 -> 708 us, M = 16 768 -> 765 us, while
+// Q8_0 lost: M = 16 781 -> 788 us).
 enum SkinnyShape { SK_R4_W16, SK_R2_W8, SK_R1_W8, SK_R1_W16 };
 static SkinnyShape skinny_shape(int64_t groups, int num_cus, bool q4) {
     if (q4 && groups >= 3 * (int64_t)num_cus && groups <= 4 * (int64_t)num_cus) return SK_R4_W16;
     if (groups >= 2 * (int64_t)num_cus) return SK_R2_W8;
-    if (groups >= num_cus) return SK_R1_W8;
+    if (groups >= num_cus && !q4) return SK_R1_W8;
     return SK_R1_W16;
 }
 
