@@ -14,26 +14,30 @@
 #include "common.h"
 #include "device_math.h"
 
+#include <climits>
+
 namespace mvlm {
 
+// The key as a signed integer that orders like the value it stands for: the
+// magnitude bits with NaN payloads clamped to infinity's pattern and zero
+// exponents to 0, negated for a set sign bit (sign-magnitude patterns of IEEE
+// formats order like their values, so this needs no conversion to float).
 template <int DT>
-__device__ __forceinline__ float argmax_key_bits(uint32_t b) {
-    if constexpr (DT == MVLM_F32) {
-        const uint32_t e = (b >> 23) & 0xFFu;
-        if (e == 0xFFu) return (b >> 31) ? -INFINITY : INFINITY;
-        return e == 0 ? 0.0f : __uint_as_float(b);
-    } else if constexpr (DT == MVLM_F16) {
-        const uint32_t e = (b >> 10) & 0x1Fu;
-        if (e == 0x1Fu) return ((b >> 15) & 1u) ? -INFINITY : INFINITY;
-        return e == 0 ? 0.0f : f16_bits_to_f32((uint16_t)b);
-    } else {
-        const uint32_t e = (b >> 7) & 0xFFu;
-        if (e == 0xFFu) return ((b >> 15) & 1u) ? -INFINITY : INFINITY;
-        return e == 0 ? 0.0f : bf16_bits_to_f32((uint16_t)b);
-    }
+__device__ __forceinline__ int argmax_key_bits(uint32_t b) {
+    constexpr int SIGN = DT == MVLM_F32 ? 31 : 15;
+    constexpr uint32_t MAG = DT == MVLM_F32 ? 0x7FFFFFFFu : 0x7FFFu;
+    constexpr uint32_t INF = DT == MVLM_F32 ? 0x7F800000u : DT == MVLM_F16 ? 0x7C00u : 0x7F80u;
+    constexpr uint32_t MIN_NORMAL = DT == MVLM_F32 ? 0x00800000u : DT == MVLM_F16 ? 0x0400u : 0x0080u;
+    uint32_t u = min(b & MAG, INF);                   // NaN -> inf
+    u = u < MIN_NORMAL ? 0u : u;                      // zeros and subnormals -> 0
+    const int neg = -(int)((b >> SIGN) & 1u);         // 0 or -1
+    return ((int)u ^ neg) - neg;                      // -u when the sign bit is set
 }
 
-__device__ __forceinline__ bool argmax_better(float k, int i, float bk, int bi) {
+// below every key (keys lie in [-INF, INF]): a thread's first element always wins
+constexpr int ARGMAX_NONE = INT_MIN;
+
+__device__ __forceinline__ bool argmax_better(int k, int i, int bk, int bi) {
     return k > bk || (k == bk && i < bi);
 }
 
@@ -54,12 +58,12 @@ __device__ __forceinline__ uint32_t chunk_elem(const u32x4& c, int e) {
 // its largest keys; the reductions break ties by the smaller index.
 template <int DT, bool VEC>
 __global__ __launch_bounds__(ARGMAX_THREADS) void argmax_kernel(const void* x, int n, int64_t ld, int* out) {
-    __shared__ float wk[ARGMAX_THREADS / 64];
+    __shared__ int wk[ARGMAX_THREADS / 64];
     __shared__ int wi[ARGMAX_THREADS / 64];
     constexpr int ES = DT == MVLM_F32 ? 4 : 2;
     constexpr int EPC = 16 / ES;
     const uint8_t* row = (const uint8_t*)x + (int64_t)blockIdx.x * ld * ES;
-    float bk = -INFINITY;
+    int bk = ARGMAX_NONE;
     int bi = 0x7FFFFFFF;
     int scalar_from = 0;
     if constexpr (VEC) {
@@ -75,8 +79,9 @@ __global__ __launch_bounds__(ARGMAX_THREADS) void argmax_kernel(const void* x, i
                 if (ci < nchunks) {
 #pragma unroll
                     for (int e = 0; e < EPC; ++e) {
-                        const float k = argmax_key_bits<DT>(chunk_elem<DT>(c[u], e));
-                        if (argmax_better(k, ci * EPC + e, bk, bi)) {
+                        // a thread's indices only increase: a strictly larger key wins
+                        const int k = argmax_key_bits<DT>(chunk_elem<DT>(c[u], e));
+                        if (k > bk) {
                             bk = k;
                             bi = ci * EPC + e;
                         }
@@ -88,15 +93,15 @@ __global__ __launch_bounds__(ARGMAX_THREADS) void argmax_kernel(const void* x, i
     }
     for (int i = scalar_from + threadIdx.x; i < n; i += ARGMAX_THREADS) {
         const uint32_t b = ES == 4 ? ((const uint32_t*)row)[i] : ((const uint16_t*)row)[i];
-        const float k = argmax_key_bits<DT>(b);
-        if (argmax_better(k, i, bk, bi)) {
+        const int k = argmax_key_bits<DT>(b);
+        if (k > bk) {
             bk = k;
             bi = i;
         }
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
-        const float ok = __shfl_xor(bk, off, 64);
+        const int ok = __shfl_xor(bk, off, 64);
         const int oi = __shfl_xor(bi, off, 64);
         if (argmax_better(ok, oi, bk, bi)) {
             bk = ok;
