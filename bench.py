@@ -94,29 +94,39 @@ def decode_inputs(dev, m, M):
 
 def build_decode_plan(dev, m, qt, M, grouped=True):
     """The plan of one Phi-1.5 decode step over quantized weights, M rows of
-    activations (see decode_step); every GEMV writes its own output buffer.
-    Returns (plan, weights, grouped, io) with io = {"x": GEMV name -> input,
-    "y": outputs in PHI_STEP order}."""
+    activations (see decode_step); every GEMV writes its own output buffer and
+    every stage reads the outputs of the stage before it, as in the model:
+    QKV and fc1 of layer l+1 read fc2's output of layer l (layer 0: the block
+    input), dense reads the first M x 2048 values of its layer's QKV output
+    (the attention output's stand-in), fc2 reads fc1's output, and the LM head
+    reads the last fc2 output.
+    Returns (plan, weights, grouped, io) with io = {"x": input of each GEMV in
+    PHI_STEP order, "y": outputs in PHI_STEP order}."""
     qdt = m.Q8_0 if qt == "q8_0" else m.Q4_0
     weights = [dev.random_weight(qdt, N, K, SEED ^ (0x100 + i), 0.02) for i, (_, N, K) in enumerate(PHI_STEP)]
     x_of = decode_inputs(dev, m, M)
     ys = [dev.alloc(M * N * 4) for _, N, _ in PHI_STEP]
+    xs = []
+    for layer in range(24):
+        i0 = 4 * layer
+        block_in = x_of["qkv"] if layer == 0 else ys[i0 - 1]
+        xs += [block_in, ys[i0].view(0, M * 2048 * 4), block_in, ys[i0 + 2]]
+    xs.append(ys[-2])
     plan = m.Plan(dev)
     if grouped:
         for layer in range(24):
             i0 = 4 * layer
-            idx = dict(zip(("qkv", "dense", "fc1", "fc2"), range(i0, i0 + 4)))
-            for pair in (("qkv", "fc1"), ("dense", "fc2")):
-                entries = [(x_of[n], m.F32, weights[idx[n]], ys[idx[n]], m.F32) for n in pair]
+            for pair in ((i0, i0 + 2), (i0 + 1, i0 + 3)):   # {QKV, fc1}, {dense, fc2}
+                entries = [(xs[i], m.F32, weights[i], ys[i], m.F32) for i in pair]
                 if M == 1:
                     plan.add_gemv_grouped(entries)
                 else:
                     plan.add_gemm_quant_grouped(M, entries)
-        plan.add_gemv(x_of["lm_head"], m.F32, weights[-1], ys[-1], m.F32, M)
+        plan.add_gemv(xs[-1], m.F32, weights[-1], ys[-1], m.F32, M)
     else:
-        for W, y, (name, N, K) in zip(weights, ys, PHI_STEP):
-            plan.add_gemv(x_of[name], m.F32, W, y, m.F32, M)
-    return plan, weights, grouped, {"x": x_of, "y": ys}
+        for x, W, y in zip(xs, weights, ys):
+            plan.add_gemv(x, m.F32, W, y, m.F32, M)
+    return plan, weights, grouped, {"x": xs, "y": ys, "inputs": x_of}
 
 
 def decode_step(dev, m, qt, M, steps, warmup, graph=True, grouped=True):
@@ -688,6 +698,9 @@ def main():
                     help="only the prefill / vision GEMM shapes and the batched QK^T (one JSON line of them)")
     ap.add_argument("--gemm-bench", action="store_true",
                     help="only the reference bench's variant x config table (one JSON line)")
+    ap.add_argument("--barrier-probe", action="store_true",
+                    help="software grid-barrier latency per round, each protocol with HBM idle and busy "
+                         "(mvlm_probe_grid_barrier; one JSON line)")
     ap.add_argument("--pmc-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn the two counter runs into " + os.path.relpath(TRAFFIC_FILE, ROOT))
     args = ap.parse_args()
@@ -713,6 +726,24 @@ def main():
     info = dev.info()
     log(f"[bench] {info.device_name.decode()} {info.arch_name.decode()} CUs={info.compute_units} "
         f"clock={info.max_clock_mhz} MHz HBM={info.global_mem_size / 2**30:.0f} GiB")
+    if args.barrier_probe:
+        names = ["counter_atomic_poll", "flag_per_workgroup", "counter_replicated_done"]
+        res = {}
+        for bg in (False, True):
+            for v, name in enumerate(names):
+                key = f"{name}_{'hbm_busy' if bg else 'hbm_idle'}_us"
+                runs = []
+                for _ in range(3):
+                    try:
+                        runs.append(dev.probe_grid_barrier(v, 200, bg))
+                    except m.native.MvlmError:   # a round waited more than 20 ms
+                        runs.append(float("inf"))
+                us = min(runs)
+                res[key] = round(us, 2) if us != float("inf") else "gave up (a round > 20 ms)"
+                log(f"[bench]   grid barrier {name:24s} HBM {'busy' if bg else 'idle'}: {res[key]} us/round")
+        print(json.dumps({"grid_barrier_us_per_round": res}), flush=True)
+        dev.close()
+        return
     if args.gemm_bench:
         print(json.dumps({"gemm_bench_matrix": gemm_bench_matrix(dev, m)}), flush=True)
         dev.close()

@@ -350,25 +350,6 @@ int mvlm_plan_add_argmax(mvlm_plan* plan, const mvlm_buffer* x, int dtype, int r
                          mvlm_buffer* out_index);
 /* enable != 0: capture the plan into a HIP graph (now) and replay it on run. */
 int mvlm_plan_use_graph(mvlm_plan* plan, int enable);
-/* Persistent decode steps (no counterpart in the reference, which blocks on
- * every dispatch, moondream2.cpp:379 ...).  With enable != 0, every run of two
- * or more consecutive entries that are M = 1 GEMVs over Q8_0 or Q4_0 weights
- * (mvlm_plan_add_gemv[_ex], mvlm_plan_add_gemv_grouped[_ex]; one weight dtype
- * per run, fp32 x and y, rows of 1, 2, 4 or 8 KiB, K <= 8192) executes as one
- * launch in which each entry is a stage: every stage sees the previous
- * stage's outputs, as between separate launches, while the next stages'
- * weights are already being read.  The launch uses one workgroup per CU and
- * needs the whole GPU: it must not share the device with concurrent work.
- * Results equal the separate launches' within the fp32 tolerance.  A stage
- * whose wait exceeds 20 ms abandons the launch and records an error, which
- * mvlm_plan_status reports.  Enabling builds device tables (allocates); a
- * plan recorded as a graph must be recorded again after this call.  Off by
- * default: on MI355X the Phi-1.5 decode step takes 497 us (Q8_0) / 475 us
- * (Q4_0) this way against 359 / 294 us as a graph of separate launches. */
-int mvlm_plan_set_persistent(mvlm_plan* plan, int enable);
-/* Waits for the plan's stream and reports MVLM_ERR_HIP if a persistent launch
- * gave up (its outputs are then not valid). */
-int mvlm_plan_status(mvlm_plan* plan);
 /* Enqueue the plan `repeats` times; `ev` (optional) spans everything enqueued. */
 int mvlm_plan_run(mvlm_plan* plan, int repeats, mvlm_event** ev);
 /* One eager run in which every launch carries start/stop events on its own
@@ -380,6 +361,19 @@ int mvlm_plan_profile(mvlm_plan* plan, float* op_ms, int capacity);
 /* Records a marker on the device stream; elapsed time between two markers. */
 int mvlm_marker_record(mvlm_device* dev, mvlm_event** out);
 int mvlm_marker_elapsed_ms(mvlm_event* start, mvlm_event* end, float* ms);
+
+/* ---- measurement of a design alternative --------------------------------- */
+/* No counterpart in the reference.  Runs `rounds` (1..1000) software grid
+ * barriers in one launch of one workgroup per CU, each preceded by a 256-byte
+ * store and its wait, and reports the time per round: the cost a persistent
+ * single-launch decode step would pay at each dependent stage, to compare with
+ * a kernel boundary.  variant 0: one counter, returning atomic add, polls;
+ * 1: one flag per workgroup, every workgroup polls all flags; 2: counter whose
+ * last arriver raises a done flag replicated on 32 lines.  background != 0:
+ * the workgroups' other 8 waves stream HBM meanwhile.  Waits are bounded
+ * (20 ms); a wait that gives up returns MVLM_ERR_HIP.  Synchronous; allocates
+ * (512 MiB with background). */
+int mvlm_probe_grid_barrier(mvlm_device* dev, int variant, int rounds, int background, double* us_per_round);
 
 #ifdef __cplusplus
 }

@@ -241,23 +241,6 @@ hipError_t launch_attention(hipStream_t s, const void* Q, const void* K, const v
                             void* workspace, size_t workspace_bytes);
 // row-wise argmax (first index of the largest key), one workgroup per row
 hipError_t launch_argmax(hipStream_t s, const void* x, int dtype, int rows, int n, int64_t ld, int* out);
-// Persistent decode step (gemv_chain.hip): a chain of dependent stages of
-// independent M = 1 GEMVs over Q8_0 / Q4_0 weights (fp32 x, y and epilogue
-// operands), one launch for the whole chain.
-struct ChainEntry {
-    const void* x;
-    const mvlm_weight* w;
-    void* y;
-    Epilogue ep;
-};
-struct ChainPlan;
-bool chain_supported(const mvlm_weight* w);
-int chain_build(const std::vector<std::vector<ChainEntry>>& stages, int num_cus, ChainPlan** out);
-void chain_free(ChainPlan* cp);
-hipError_t launch_chain(hipStream_t s, const ChainPlan* cp);
-// the chain's error word (nonzero: a stage wait timed out); synchronous
-int chain_error(const ChainPlan* cp, uint32_t* error);
-
 hipError_t launch_pack(hipStream_t s, const void* src, int dtype, int layout, int N, int K,
                        mvlm_weight* w);
 hipError_t launch_dequant(hipStream_t s, const mvlm_weight* w, float* out);

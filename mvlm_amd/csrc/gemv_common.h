@@ -1,5 +1,4 @@
-// Per-chunk arithmetic and LDS staging shared by the streaming GEMV
-// (gemv_stream.hip) and the persistent decode-step kernel (gemv_chain.hip).
+// Per-chunk arithmetic and LDS staging of the streaming GEMV (gemv_stream.hip).
 // A "chunk" is one 16-byte vector per lane, 1 KiB per wave, of one weight row:
 // 4 fp32, 8 fp16/bf16, 16 Q8_0 codes (half a block) or 32 Q4_0 codes (one
 // block) per lane.  Codes become fp32 in registers: v_cvt_f32_i32 with a byte

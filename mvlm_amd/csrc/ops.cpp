@@ -550,80 +550,12 @@ extern "C" int mvlm_argmax(mvlm_device* dev, const mvlm_buffer* x, int dtype, in
 // plans
 // ---------------------------------------------------------------------------
 
-// A run of consecutive plan entries [first, last) served by one persistent
-// launch (gemv_chain.hip).
-struct ChainRun {
-    int first = 0, last = 0;
-    ChainPlan* chain = nullptr;
-};
-
 struct mvlm_plan {
     mvlm_device* dev = nullptr;
     std::vector<Op> ops;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
-    bool persistent = false;      // serve runs of chainable entries with one launch each
-    bool chains_dirty = false;    // entries were added since the runs were built
-    std::vector<ChainRun> runs;
 };
-
-static void drop_chains(mvlm_plan* p) {
-    for (ChainRun& r : p->runs) chain_free(r.chain);
-    p->runs.clear();
-}
-
-// An entry a persistent launch can serve: M = 1 GEMVs over Q8_0 / Q4_0
-// weights (fp32 x and y) whose rows and x fit the chain kernel.
-static bool chainable(const Op& op, int* dtype) {
-    if (op.kind == OP_GEMV_QUANT) {
-        if (op.M != 1 || !chain_supported(op.w)) return false;
-        *dtype = op.w->dtype;
-        return true;
-    }
-    if (op.kind != OP_GEMV_GROUP || op.M != 1 || op.a_dtype != MVLM_F32) return false;
-    for (int i = 0; i < op.gcount; ++i)
-        if (op.gyd[i] != MVLM_F32 || !chain_supported(op.gw[i]) || op.gw[i]->dtype != op.gw[0]->dtype) return false;
-    *dtype = op.gw[0]->dtype;
-    return true;
-}
-
-// Maximal runs of at least two chainable entries of one weight dtype, each
-// entry one stage of a chain.
-static int build_chains(mvlm_plan* p) {
-    drop_chains(p);
-    p->chains_dirty = false;
-    const int n = (int)p->ops.size();
-    int i = 0;
-    while (i < n) {
-        int dt = 0;
-        if (!chainable(p->ops[i], &dt)) { ++i; continue; }
-        int j = i + 1, dt2 = 0;
-        while (j < n && chainable(p->ops[j], &dt2) && dt2 == dt) ++j;
-        if (j - i >= 2) {
-            std::vector<std::vector<ChainEntry>> stages;
-            try {
-                for (int k = i; k < j; ++k) {
-                    const Op& op = p->ops[k];
-                    std::vector<ChainEntry> st;
-                    if (op.kind == OP_GEMV_QUANT) st.push_back(ChainEntry{op.a, op.w, op.c, op.ep});
-                    else
-                        for (int e = 0; e < op.gcount; ++e) st.push_back(ChainEntry{op.gx[e], op.gw[e], op.gy[e], op.gep[e]});
-                    stages.push_back(std::move(st));
-                }
-                ChainRun run;
-                run.first = i;
-                run.last = j;
-                const int st = chain_build(stages, p->dev->prop.multiProcessorCount, &run.chain);
-                if (st != MVLM_OK) return st;
-                p->runs.push_back(run);
-            } catch (...) {
-                return set_error(MVLM_ERR_OUT_OF_MEMORY, "plan: chain bookkeeping failed");
-            }
-        }
-        i = j;
-    }
-    return MVLM_OK;
-}
 
 static void drop_graph(mvlm_plan* p) {
     if (p->exec) (void)hipGraphExecDestroy(p->exec);
@@ -645,7 +577,6 @@ extern "C" int mvlm_plan_create(mvlm_device* dev, mvlm_plan** out) {
 extern "C" int mvlm_plan_destroy(mvlm_plan* plan) {
     REQUIRE(plan, "mvlm_plan_destroy: plan is null");
     drop_graph(plan);
-    drop_chains(plan);
     delete plan;
     return MVLM_OK;
 }
@@ -654,7 +585,6 @@ extern "C" int mvlm_plan_size(const mvlm_plan* plan) { return plan ? (int)plan->
 
 static int plan_push(mvlm_plan* plan, const Op& op) {
     drop_graph(plan);   // a recorded graph no longer matches
-    if (plan->persistent) plan->chains_dirty = true;
     try {
         plan->ops.push_back(op);
     } catch (...) {
@@ -769,49 +699,11 @@ extern "C" int mvlm_plan_add_argmax(mvlm_plan* plan, const mvlm_buffer* x, int d
     return st != MVLM_OK ? st : plan_push(plan, op);
 }
 
-// The plan's launches in order: each chain run as one launch, other entries
-// one launch each.  (Chains are (re)built here only outside stream capture.)
+// The plan's launches in order, one per entry.
 static int enqueue_all(mvlm_plan* plan) {
-    if (plan->persistent && plan->chains_dirty) {
-        const int st = build_chains(plan);
-        if (st != MVLM_OK) return st;
-    }
-    size_t next_run = 0;
-    const int n = (int)plan->ops.size();
-    for (int i = 0; i < n; ++i) {
-        hipError_t e;
-        if (plan->persistent && next_run < plan->runs.size() && plan->runs[next_run].first == i) {
-            e = launch_chain(plan->dev->stream, plan->runs[next_run].chain);
-            i = plan->runs[next_run].last - 1;
-            ++next_run;
-        } else {
-            e = enqueue_op(plan->dev->stream, plan->ops[i]);
-        }
+    for (const Op& op : plan->ops) {
+        const hipError_t e = enqueue_op(plan->dev->stream, op);
         if (e != hipSuccess) return check_hip(e, "plan launch");
-    }
-    return MVLM_OK;
-}
-
-extern "C" int mvlm_plan_set_persistent(mvlm_plan* plan, int enable) {
-    REQUIRE(plan, "mvlm_plan_set_persistent: plan is null");
-    drop_graph(plan);
-    plan->persistent = enable != 0;
-    if (!plan->persistent) {
-        drop_chains(plan);
-        return MVLM_OK;
-    }
-    return build_chains(plan);
-}
-
-extern "C" int mvlm_plan_status(mvlm_plan* plan) {
-    REQUIRE(plan, "mvlm_plan_status: plan is null");
-    HIP_TRY(hipStreamSynchronize(plan->dev->stream));
-    for (const ChainRun& r : plan->runs) {
-        uint32_t err = 0;
-        const int st = chain_error(r.chain, &err);
-        if (st != MVLM_OK) return st;
-        if (err) return set_error(MVLM_ERR_HIP, "plan: a persistent launch gave up waiting for a stage "
-                                  "(entries %d..%d); its outputs are not valid", r.first, r.last - 1);
     }
     return MVLM_OK;
 }
@@ -821,10 +713,6 @@ extern "C" int mvlm_plan_use_graph(mvlm_plan* plan, int enable) {
     drop_graph(plan);
     if (!enable) return MVLM_OK;
     REQUIRE(!plan->ops.empty(), "mvlm_plan_use_graph: the plan is empty");
-    if (plan->persistent && plan->chains_dirty) {   // no allocation during capture
-        const int st = build_chains(plan);
-        if (st != MVLM_OK) return st;
-    }
     hipStream_t s = plan->dev->stream;
     HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
     int st = enqueue_all(plan);
@@ -865,38 +753,21 @@ extern "C" int mvlm_plan_profile(mvlm_plan* plan, float* op_ms, int capacity) {
     int st = MVLM_OK;
     for (size_t i = 0; i < ev.size() && st == MVLM_OK; ++i) st = check_hip(hipEventCreate(&ev[i]), "hipEventCreate");
     hipStream_t s = plan->dev->stream;
-    if (st == MVLM_OK && plan->persistent && plan->chains_dirty) st = build_chains(plan);
     KernelTiming& t = kernel_timing();
-    // a chain run is one launch: its time goes to the run's first entry, the
-    // others read 0
-    std::vector<char> timed((size_t)n, 0);
-    size_t next_run = 0;
-    int last_timed = -1;
+    int launched = 0;
     for (int i = 0; i < n && st == MVLM_OK; ++i) {
         t.start = ev[2 * i];
         t.stop = ev[2 * i + 1];
-        hipError_t e;
-        if (plan->persistent && next_run < plan->runs.size() && plan->runs[next_run].first == i) {
-            e = launch_chain(s, plan->runs[next_run].chain);
-            timed[i] = 1;
-            last_timed = i;
-            i = plan->runs[next_run].last - 1;
-            ++next_run;
-        } else {
-            e = enqueue_op(s, plan->ops[i]);
-            timed[i] = 1;
-            last_timed = i;
-        }
+        const hipError_t e = enqueue_op(s, plan->ops[i]);
         t = KernelTiming{};
         if (e != hipSuccess) st = check_hip(e, "plan launch");
+        else launched = i + 1;
     }
     t = KernelTiming{};
-    if (st == MVLM_OK && last_timed >= 0)
-        st = check_hip(hipEventSynchronize(ev[2 * (size_t)last_timed + 1]), "hipEventSynchronize");
-    for (int i = 0; i < n && st == MVLM_OK; ++i) {
-        op_ms[i] = 0.0f;
-        if (timed[i]) st = check_hip(hipEventElapsedTime(&op_ms[i], ev[2 * i], ev[2 * i + 1]), "hipEventElapsedTime");
-    }
+    if (st == MVLM_OK && launched > 0)
+        st = check_hip(hipEventSynchronize(ev[2 * (size_t)(launched - 1) + 1]), "hipEventSynchronize");
+    for (int i = 0; i < n && st == MVLM_OK; ++i)
+        st = check_hip(hipEventElapsedTime(&op_ms[i], ev[2 * i], ev[2 * i + 1]), "hipEventElapsedTime");
     for (hipEvent_t e : ev)
         if (e) (void)hipEventDestroy(e);
     return st;

@@ -105,6 +105,7 @@ _SIGNATURES = {
     "mvlm_gemm_packed_ex": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, c_int, c_int, POINTER(Epilogue), _PP]),
     "mvlm_gemv_ex": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, c_int, POINTER(Epilogue), _PP]),
     "mvlm_gemm_packed_ex_noalloc": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, c_int, c_int, POINTER(Epilogue)]),
+    "mvlm_probe_grid_barrier": (c_int, [_P, c_int, c_int, c_int, POINTER(c_double)]),
     "mvlm_plan_add_gemv_ex": (c_int, [_P, _P, c_int, _P, _P, c_int, POINTER(Epilogue)]),
     "mvlm_plan_add_gemm_packed_ex": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, POINTER(Epilogue)]),
     "mvlm_plan_add_gemv_grouped": (c_int, [_P, c_int, POINTER(GemvDesc)]),
@@ -139,8 +140,6 @@ _SIGNATURES = {
     "mvlm_plan_add_gemm_batched": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int,
                                            c_int64, c_int64, c_int64, c_int64, c_int64, c_int64]),
     "mvlm_plan_use_graph": (c_int, [_P, c_int]),
-    "mvlm_plan_set_persistent": (c_int, [_P, c_int]),
-    "mvlm_plan_status": (c_int, [_P]),
     "mvlm_plan_run": (c_int, [_P, c_int, _PP]),
     "mvlm_plan_profile": (c_int, [_P, POINTER(c_float), c_int]),
     "mvlm_marker_record": (c_int, [_P, _PP]),
@@ -417,15 +416,6 @@ class Plan:
         self.handle = h
         self._keep = []
 
-    def set_persistent(self, enable=True):
-        """serve runs of consecutive M = 1 Q8_0 / Q4_0 GEMV entries with one persistent launch each"""
-        _call("mvlm_plan_set_persistent", self.handle, 1 if enable else 0)
-        return self
-
-    def status(self):
-        """wait for the plan's work; raises if a persistent launch gave up"""
-        _call("mvlm_plan_status", self.handle)
-
     def __len__(self):
         return lib().mvlm_plan_size(self.handle)
 
@@ -617,6 +607,12 @@ class Device:
         ep = _epilogue(bias, act, mul, residual)
         _call("mvlm_gemm_packed_ex_noalloc", self.handle, A.handle, a_dtype, W.handle, C.handle, c_dtype, M, N, K,
               byref(ep))
+
+    def probe_grid_barrier(self, variant, rounds=200, background=False):
+        """microseconds per software grid barrier round (mvlm_probe_grid_barrier)"""
+        us = c_double()
+        _call("mvlm_probe_grid_barrier", self.handle, variant, rounds, 1 if background else 0, byref(us))
+        return us.value
 
     def gemv_ex(self, x, x_dtype, W, y, y_dtype, N, K, bias=None, act=ACT_NONE, mul=None, residual=None,
                 event=False):
