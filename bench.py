@@ -49,12 +49,22 @@ def gemv_bytes(qt, N, K, M):
     return quant_bytes(qt, N, K) + 4 * M * K + 4 * M * N
 
 
+# Peaks derived from the device's own properties (mvlm_device_info box_peak_*),
+# reported beside the nominal ones; set by main() once the device is open.
+BOX_PEAK = {}
+
+
 def roofline(bound, achieved, timing):
     """roofline block of one workload: achieved GB/s (bound "hbm") or TFLOP/s
-    (bound "mfma") against MI355X's nominal peak"""
+    (bound "mfma") against MI355X's nominal peak, and against the peak derived
+    from this device's reported clocks and CU count"""
     peak, unit = (PEAK_HBM_GBS, "GB/s") if bound == "hbm" else (PEAK_F16_TFLOPS, "TFLOP/s")
-    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
-            "frac": round(achieved / peak, 4), "timing": timing}
+    r = {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+         "frac": round(achieved / peak, 4), "timing": timing}
+    if BOX_PEAK.get(bound):
+        r["peak_box"] = round(BOX_PEAK[bound], 1)
+        r["frac_box"] = round(achieved / BOX_PEAK[bound], 4)
+    return r
 
 
 def timed_plan(dev, plan, steps, warmup):
@@ -218,9 +228,15 @@ def decode_token(dev, m, qt, cache, steps, warmup):
     plan.destroy()
     for W in weights:
         W.free()
+    nbytes = (sum(gemv_bytes(qt, N, K, 1) for _, N, K in PHI_STEP)   # weights, x, y
+              + 24 * 2 * cache * 32 * 64 * 2.0                        # the KV cache, fp16
+              + 51200 * 4.0)                                          # logits read by the token pick
     return {"workload": f"phi15_decode_token_{qt}_cache{cache}", "us": ms * 1e3, "tokens_per_s": 1e3 / ms,
             "ops": 24 * 3 + 2, "epilogues": "QKV+bias, fc1+bias+GELU, dense+bias+residual, fc2+bias+residual "
-                                            "fused into the grouped GEMVs"}
+                                            "fused into the grouped GEMVs",
+            "bytes_per_token": nbytes,
+            "roofline": roofline("hbm", nbytes / ms / 1e6, "timed region (HIP events around the graph replays) "
+                                 "/ tokens; bytes = weights, x and y of the 97 GEMVs, the KV cache, the logits")}
 
 
 def fp32_gemv(dev, m, steps, warmup, copies=16):
@@ -240,6 +256,8 @@ def fp32_gemv(dev, m, steps, warmup, copies=16):
     res = {"workload": "gemv_f32_2048x8192", "us": ms * 1e3, "gbs": nbytes / ms / 1e6,
            "kernel_us": float(np.median(per_op)) * 1e3, "kernel_gbs": nbytes / float(np.median(per_op)) / 1e6}
     res["frac"] = res["gbs"] / PEAK_HBM_GBS
+    res["roofline"] = roofline("hbm", res["gbs"], "timed region (HIP events around the graph replays of "
+                               f"{copies} launches, one per weight copy) / launches")
     plan.destroy()
     return res
 
@@ -262,21 +280,24 @@ def gemv_exact(dev, m, steps, warmup, copies=16):
     us = float(np.median(times)) * 1e3
     nbytes = 2.0 * N * K + 2 * K + 2 * N
     return {"workload": "gemv_exact_f16_2048x8192", "kernel_us": us, "gbs": nbytes / us / 1e3,
-            "frac": nbytes / us / 1e3 / PEAK_HBM_GBS}
+            "frac": nbytes / us / 1e3 / PEAK_HBM_GBS,
+            "roofline": roofline("hbm", nbytes / us / 1e3, "median of per-launch HIP start/stop events, "
+                                 f"rotating over {copies} weight copies")}
 
 
-def gemm_shape(dev, m, name, M, N, K, steps, warmup):
-    """fp16-in / fp32-out MFMA GEMM, A[M,K] N(0,1), W[N,K] N(0,0.02)."""
-    W = dev.random_weight(m.F16, N, K, SEED ^ (zlib.crc32(name.encode()) & 0xFFFF), 0.02)
-    A = dev.fill_normal(dev.alloc(M * K * 2), m.F16, M * K, SEED ^ 0x300, 1.0)
+def gemm_shape(dev, m, name, M, N, K, steps, warmup, bf16=False):
+    """fp16-in (bf16 with bf16=True) / fp32-out MFMA GEMM, A[M,K] N(0,1), W[N,K] N(0,0.02)."""
+    dt = m.BF16 if bf16 else m.F16
+    W = dev.random_weight(dt, N, K, SEED ^ (zlib.crc32(name.encode()) & 0xFFFF), 0.02)
+    A = dev.fill_normal(dev.alloc(M * K * 2), dt, M * K, SEED ^ 0x300, 1.0)
     C = dev.alloc(M * N * 4)
     plan = m.Plan(dev)
-    plan.add_gemm_packed(A, m.F16, W, C, m.F32, M)
+    plan.add_gemm_packed(A, dt, W, C, m.F32, M)
     per_op = profile_plan(plan)
     ms = timed_plan(dev, plan, steps, warmup)
     flops = 2.0 * M * N * K
-    res = {"workload": name, "shape": [M, N, K], "us": ms * 1e3, "tflops": flops / ms / 1e9,
-           "kernel_us": float(per_op[0]) * 1e3}
+    res = {"workload": name, "shape": [M, N, K], "dtype": "bf16" if bf16 else "f16", "us": ms * 1e3,
+           "tflops": flops / ms / 1e9, "kernel_us": float(per_op[0]) * 1e3}
     res["frac"] = res["tflops"] / PEAK_F16_TFLOPS
     res["roofline"] = roofline("mfma", res["tflops"], "timed region (HIP events around the graph replays) / launches")
     plan.destroy()
@@ -297,6 +318,9 @@ def qk_batched(dev, m, steps, warmup):
            "gbs": nbytes / ms / 1e6}
     res["frac_mfma"] = res["tflops"] / PEAK_F16_TFLOPS
     res["frac_hbm"] = res["gbs"] / PEAK_HBM_GBS
+    timing = "timed region (HIP events around the graph replays) / launches"
+    res["roofline"] = roofline("hbm", res["gbs"], timing + "; bytes = fp16 Q and K + fp32 scores")
+    res["roofline_mfma"] = roofline("mfma", res["tflops"], timing)
     plan.destroy()
     return res
 
@@ -339,6 +363,11 @@ def attention_shape(dev, m, name, sq, skv, H, D, causal, steps, warmup):
            "tflops": flops / kus / 1e6, "gbs": nbytes / kus / 1e3}
     res["frac_mfma"] = res["tflops"] / PEAK_F16_TFLOPS
     res["frac_hbm"] = res["gbs"] / PEAK_HBM_GBS
+    timing = "median of per-launch HIP start/stop events over one eager pass of the graph's copies"
+    if sq == 1:   # one query: streaming the KV cache
+        res["roofline"] = roofline("hbm", res["gbs"], timing + "; bytes = Q, K, V and O once each")
+    else:
+        res["roofline"] = roofline("mfma", res["tflops"], timing + "; flops = QK^T and PV (causal: visible half)")
     plan.destroy()
     return res
 
@@ -356,6 +385,8 @@ def token_pick(dev, m, steps, warmup):
     ms = timed_plan(dev, plan, steps, warmup) / OP_REPEATS
     kus = float(np.median(per_op)) * 1e3
     res = {"workload": "token_pick_51200_f32", "us": ms * 1e3, "kernel_us": kus, "gbs": 4.0 * n / kus / 1e3}
+    res["roofline"] = roofline("hbm", res["gbs"], "median of per-launch HIP start/stop events; bytes = the "
+                               "fp32 logits read once")
     plan.destroy()
     return res
 
@@ -421,11 +452,12 @@ GEMM_SHAPES = (("phi15_prefill_qkv", 768, 6144, 2048), ("phi15_prefill_fc1", 768
 
 def gemm_extras(dev, m, steps, warmup, extra):
     """The M = 729 / 768 fp16 GEMMs (Phi-1.5 prefill, SigLIP) and the batched QK^T."""
-    for name, M, N, K in GEMM_SHAPES:
-        r = gemm_shape(dev, m, name, M, N, K, steps, warmup)
-        extra[name] = r
-        log(f"[bench]   {name} {M}x{N}x{K}: {r['us']:.1f} us {r['tflops']:.0f} TFLOP/s "
-            f"({100 * r['frac']:.1f}% of 2.5 PF)")
+    for bf16 in (False, True):
+        for name, M, N, K in GEMM_SHAPES:
+            r = gemm_shape(dev, m, name + ("_bf16" if bf16 else ""), M, N, K, steps, warmup, bf16)
+            extra[r["workload"]] = r
+            log(f"[bench]   {r['workload']} {M}x{N}x{K}: {r['us']:.1f} us {r['tflops']:.0f} TFLOP/s "
+                f"({100 * r['frac']:.1f}% of 2.5 PF)")
     r = qk_batched(dev, m, steps, warmup)
     extra[r["workload"]] = r
     log(f"[bench]   {r['workload']}: {r['us']:.1f} us {r['tflops']:.0f} TFLOP/s {r['gbs']:.0f} GB/s")
@@ -548,7 +580,8 @@ def pmc_probe(steps=3):
     print("pmc probe done", flush=True)
 
 
-PMC_WORKLOADS = ("decode_q8_0_m1", "decode_q4_0_m1", "decode_q4_0_m4", "decode_q4_0_m16", "decode_q8_0_m4", "gemm")
+PMC_WORKLOADS = ("decode_q8_0_m1", "decode_q4_0_m1", "decode_q4_0_m4", "decode_q4_0_m16", "decode_q8_0_m4", "gemm",
+                 "gemm_bf16", "gemv_f32", "gemv_exact", "qk_batched", "attention", "argmax")
 
 
 def pmc_workload(name, reps=2):
@@ -565,15 +598,62 @@ def pmc_workload(name, reps=2):
         plan, ws, _, _ = build_decode_plan(dev, m, f"{qt0}_{qt1}", int(mm[1:]), True)
         plans.append((name, plan))
         weights += ws
-    elif name == "gemm":
+    elif name in ("gemm", "gemm_bf16"):
+        dt = m.BF16 if name == "gemm_bf16" else m.F16
         for wname, M, N, K in GEMM_SHAPES:
-            W = dev.random_weight(m.F16, N, K, SEED ^ (zlib.crc32(wname.encode()) & 0xFFFF), 0.02)
-            A = dev.fill_normal(dev.alloc(M * K * 2), m.F16, M * K, SEED ^ 0x300, 1.0)
+            W = dev.random_weight(dt, N, K, SEED ^ (zlib.crc32(wname.encode()) & 0xFFFF), 0.02)
+            A = dev.fill_normal(dev.alloc(M * K * 2), dt, M * K, SEED ^ 0x300, 1.0)
             C = dev.alloc(M * N * 4)
             plan = m.Plan(dev)
-            plan.add_gemm_packed(A, m.F16, W, C, m.F32, M)
+            plan.add_gemm_packed(A, dt, W, C, m.F32, M)
             plans.append((wname, plan))
             weights.append(W)
+    elif name in ("gemv_f32", "gemv_exact"):   # 16 rotating copies of the 2048 -> 8192 weight
+        N, K = 8192, 2048
+        dt = m.F32 if name == "gemv_f32" else m.F16
+        x = dev.fill_normal(dev.alloc(K * 4), dt, K, SEED ^ 0x201, 1.0)
+        y = dev.alloc(N * 4)
+        plan = m.Plan(dev)
+        for i in range(16):
+            W = dev.random_weight(dt, N, K, SEED ^ (0x200 + i), 0.02)
+            weights.append(W)
+            if name == "gemv_f32":
+                plan.add_gemv(x, m.F32, W, y, m.F32)
+        if name == "gemv_exact":
+            class Exact:   # one eager pass: each copy through mvlm_gemv_exact
+                def run(self, n):
+                    for W in weights:
+                        dev.gemv_exact(x, W, y, N, K)
+
+                def destroy(self):
+                    pass
+            plan.destroy()
+            plan = Exact()
+        plans.append((name, plan))
+    elif name == "qk_batched":
+        H, S, D = 16, 729, 72
+        Q = dev.fill_normal(dev.alloc(S * H * D * 2), m.F16, S * H * D, SEED ^ 0x401, 1.0)
+        Kt = dev.fill_normal(dev.alloc(S * H * D * 2), m.F16, S * H * D, SEED ^ 0x402, 1.0)
+        C = dev.alloc(H * S * S * 4)
+        plan = m.Plan(dev)
+        plan.add_gemm_batched(Q, Kt, C, H, S, S, D, H * D, H * D, S, D, D, S * S)
+        plans.append((name, plan))
+    elif name == "attention":
+        for aname, sq, skv, H, D, causal in ATTENTION_SHAPES:
+            Q = dev.fill_normal(dev.alloc(sq * H * D * 2), m.F16, sq * H * D, SEED ^ 0x501, 1.0)
+            K = dev.fill_normal(dev.alloc(skv * H * D * 2), m.F16, skv * H * D, SEED ^ 0x502, 1.0)
+            V = dev.fill_normal(dev.alloc(skv * H * D * 2), m.F16, skv * H * D, SEED ^ 0x503, 1.0)
+            O = dev.alloc(sq * H * D * 2)
+            plan = m.Plan(dev)
+            plan.add_attention(Q, K, V, O, m.F16, sq, skv, H, D, causal=causal)
+            plans.append((aname, plan))
+    elif name == "argmax":
+        n = PHI_LM_HEAD[1]
+        x = dev.fill_normal(dev.alloc(n * 4), m.F32, n, SEED ^ 0x601, 1.0)
+        out = dev.alloc(4)
+        plan = m.Plan(dev)
+        plan.add_argmax(x, m.F32, 1, n, n, out)
+        plans.append((name, plan))
     else:
         raise SystemExit(f"unknown counter workload {name}; one of {', '.join(PMC_WORKLOADS)}")
     for r in range(reps):
@@ -724,8 +804,11 @@ def main():
     import mvlm_amd as m
     dev = m.Device(0)
     info = dev.info()
+    BOX_PEAK["hbm"], BOX_PEAK["mfma"] = info.box_peak_hbm_gbs, info.box_peak_fp16_tflops
     log(f"[bench] {info.device_name.decode()} {info.arch_name.decode()} CUs={info.compute_units} "
-        f"clock={info.max_clock_mhz} MHz HBM={info.global_mem_size / 2**30:.0f} GiB")
+        f"clock={info.max_clock_mhz} MHz HBM={info.global_mem_size / 2**30:.0f} GiB; derived peaks "
+        f"{info.box_peak_fp16_tflops:.0f} TFLOP/s fp16 (CUs x clock x 4096), {info.box_peak_hbm_gbs:.0f} GB/s "
+        f"(memory clock {info.memory_clock_mhz} MHz x {info.memory_bus_width_bits} bits x 4 / 8)")
     if args.barrier_probe:
         names = ["counter_atomic_poll", "flag_per_workgroup", "counter_replicated_done"]
         res = {}
@@ -821,6 +904,9 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(head["frac"], 4), "traffic": measured_traffic(),
+                     "peak_box": round(BOX_PEAK["hbm"], 1), "frac_box": round(head["gbs"] / BOX_PEAK["hbm"], 4),
+                     "peak_note": "peak = MI355X nominal 8 TB/s; peak_box = this device's memory clock x bus "
+                                  "width x 4 / 8 (HBM3E, mvlm_device_info)",
                      "traffic_note": "HBM bytes per step (49 launches) from rocprofv3 FETCH_SIZE + WRITE_SIZE, "
                                      "scaled by a 256 MiB device copy; " + os.path.relpath(TRAFFIC_FILE, ROOT),
                      "kernel": "gemv_stream_kernel<Q8Fmt>",

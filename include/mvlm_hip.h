@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MVLM_ABI_VERSION 1
+#define MVLM_ABI_VERSION 2
 
 /* ---- status codes ------------------------------------------------------- */
 enum mvlm_status {
@@ -78,6 +78,13 @@ typedef struct mvlm_device_info {
     uint64_t l2_cache_size;
     double peak_hbm_gbs;             /* nominal MI355X HBM3E: 8000 GB/s */
     double peak_fp16_tflops;         /* nominal dense fp16/bf16 MFMA: 2500 */
+    /* the same peaks derived from this device's reported properties, as the
+     * reference bench derives its peak (gemm_bench.cpp:180-182): CUs x clock x
+     * 4096 dense fp16 flops per CU per clock (4 SIMDs of CDNA4), and memory
+     * clock x bus width x 4 / 8 (HBM3E: data on both edges of a write clock
+     * running at twice the reported memory clock) */
+    double box_peak_hbm_gbs;
+    double box_peak_fp16_tflops;
 } mvlm_device_info;
 
 /* ---- errors -------------------------------------------------------------- */

@@ -179,6 +179,8 @@ extern "C" int mvlm_device_get_info(const mvlm_device* dev, mvlm_device_info* in
     info->l2_cache_size = (uint64_t)p.l2CacheSize;
     info->peak_hbm_gbs = 8000.0;
     info->peak_fp16_tflops = 2500.0;
+    info->box_peak_hbm_gbs = (double)info->memory_clock_mhz * 1e6 * info->memory_bus_width_bits * 4.0 / 8.0 / 1e9;
+    info->box_peak_fp16_tflops = (double)info->compute_units * info->max_clock_mhz * 1e6 * 4096.0 / 1e12;
     return MVLM_OK;
 }
 

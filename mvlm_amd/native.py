@@ -36,7 +36,8 @@ class DeviceInfo(ctypes.Structure):
                 ("ordinal", c_int), ("compute_units", c_int), ("max_clock_mhz", c_int),
                 ("memory_clock_mhz", c_int), ("memory_bus_width_bits", c_int), ("wavefront_size", c_int),
                 ("global_mem_size", c_uint64), ("local_mem_size", c_uint64), ("l2_cache_size", c_uint64),
-                ("peak_hbm_gbs", c_double), ("peak_fp16_tflops", c_double)]
+                ("peak_hbm_gbs", c_double), ("peak_fp16_tflops", c_double),
+                ("box_peak_hbm_gbs", c_double), ("box_peak_fp16_tflops", c_double)]
 
 
 class GgufInfo(ctypes.Structure):

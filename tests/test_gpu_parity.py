@@ -344,9 +344,12 @@ def test_gemm_packed_small(dev, orc, M, N, K, ab, cd):
 
 @pytest.mark.parametrize("M,N,K", [(768, 6144, 2048), (768, 8192, 2048), (768, 2048, 8192),
                                    (729, 3456, 1152), (729, 1152, 1152), (729, 4304, 1152), (729, 1152, 4304)])
-def test_gemm_packed_model_shapes(dev, orc, M, N, K):
-    """The Phi-1.5 prefill and SigLIP linears; every output column, 24 rows spread over M."""
-    check_packed(dev, orc, M, N, K, F16, F32, rows=24)
+@pytest.mark.parametrize("ab,cd", [(F16, F32), (BF16, F32), (BF16, BF16)])
+def test_gemm_packed_model_shapes(dev, orc, M, N, K, ab, cd):
+    """The Phi-1.5 prefill and SigLIP linears with fp16 and bf16 inputs (fp32 and
+    bf16 out): every output column, 24 rows spread over M, within 1e-3 * S of the
+    fp32 fma chain in ascending k (gemm.cl:26-51's arithmetic on 16-bit inputs)."""
+    check_packed(dev, orc, M, N, K, ab, cd, rows=24)
 
 
 @pytest.mark.parametrize("M,N,K", [(3, 5, 1), (17, 33, 7), (64, 70, 9), (100, 130, 588), (729, 1152, 588)])
