@@ -229,6 +229,13 @@ inline int64_t weight_row_bytes(const mvlm_weight* w) { return is_dense(w->dtype
 // kread_b < K rounded up to 8.
 size_t gemm_workspace_bytes(int batch, int M, int N, int K, int64_t lda, int64_t ldb, int64_t sA, int64_t sB,
                             int kread_b, int num_cus);
+// Batched NT products with K <= 128 (a multiple of 8) and a dense fp32 C per
+// batch (ldc == N <= 1024), A/B/C 16-byte aligned: C's rows in blocks of 16,
+// each written as one contiguous range (gemm_smallk.hip).
+bool smallk_supported(int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc, int64_t sA, int64_t sB,
+                      const void* A, const void* B, const void* C);
+hipError_t launch_gemm_smallk(hipStream_t s, const void* A, int ab_dtype, const void* B, float* C, int batch, int M,
+                              int N, int K, int64_t lda, int64_t ldb, int64_t sA, int64_t sB, int64_t sC, int num_cus);
 hipError_t launch_gemm_mfma(hipStream_t s, const void* A, int ab_dtype, const void* B, void* C,
                             int c_dtype, int batch, int M, int N, int K, int64_t lda, int64_t ldb,
                             int64_t ldc, int64_t strideA, int64_t strideB, int64_t strideC,

@@ -347,6 +347,10 @@ hipError_t enqueue_op(hipStream_t s, const Op& op) {
         case OP_GEMV_EXACT:
             return launch_gemv_exact(s, (const uint16_t*)op.a, op.w, (uint16_t*)op.c);
         case OP_GEMM_MFMA:
+            if (op.c_dtype == MVLM_F32 && !op.ep.any() &&
+                smallk_supported(op.M, op.N, op.K, op.lda, op.ldb, op.ldc, op.sA, op.sB, op.a, op.b, op.c))
+                return launch_gemm_smallk(s, op.a, op.a_dtype, op.b, (float*)op.c, op.batch, op.M, op.N, op.K, op.lda,
+                                          op.ldb, op.sA, op.sB, op.sC, op.num_cus);
             return launch_gemm_mfma(s, op.a, op.a_dtype, op.b, op.c, op.c_dtype, op.batch, op.M, op.N, op.K,
                                     op.lda, op.ldb, op.ldc, op.sA, op.sB, op.sC, op.kread_b, op.num_cus, &op.ep,
                                     op.workspace, op.workspace_bytes);
