@@ -177,18 +177,22 @@ def decode_step(dev, m, qt, M, steps, warmup, graph=True, grouped=True):
     return res
 
 
-def build_token_plan(dev, m, qt, cache):
+def build_token_plan(dev, m, qt, cache, fuse=True):
     """The plan of one Phi-1.5 decode step with the path's own ops end to end: per
     layer the grouped {QKV, fc1} GEMV, attention of the new token against a
-    `cache`-entry fp16 KV cache (32 heads of 64), the grouped {dense, fc2} GEMV;
-    then the LM head and the on-device token pick.  Layer norm, rotary
-    embedding, the KV append and GELU are not part of this path and are left
-    out.  The grouped launches carry the epilogues of the block's projections:
-    QKV + bias, fc1 + bias + GELU, dense + bias + residual, fc2 + bias +
-    residual (the residual stream h; each branch writes its own output).
-    Returns (plan, weights, io) with io = {"x", "y" (PHI_STEP order), "ep"
-    (per GEMV: dict of bias / act / residual buffers, or None), "token", "q",
-    "k", "v", "o"}."""
+    `cache`-entry fp16 KV cache (32 heads of 64, fp32 output), the grouped
+    {dense, fc2} GEMV with dense reading the attention output; then the LM
+    head and the on-device token pick.  Layer norm, rotary embedding, the KV
+    append and GELU are not part of this path and are left out (q, K and V are
+    fixed stand-ins, the same for every layer).  The grouped launches carry
+    the epilogues of the block's projections: QKV + bias, fc1 + bias + GELU,
+    dense + bias + residual, fc2 + bias + residual (the residual stream h;
+    each branch writes its own output).  fuse: plan fusion, each attention
+    computed inside the {dense, fc2} launch that reads it (74 entries, 50
+    launches); off, every entry is a launch.
+    Returns (plan, weights, io) with io = {"x" (input of each GEMV), "y"
+    (PHI_STEP order), "ep" (per GEMV: dict of bias / act / residual buffers,
+    or None), "token", "q", "k", "v", "o"}."""
     qdt = m.Q8_0 if qt == "q8_0" else m.Q4_0
     weights = [dev.random_weight(qdt, N, K, SEED ^ (0x100 + i), 0.02) for i, (_, N, K) in enumerate(PHI_STEP)]
     x_of = decode_inputs(dev, m, 1)
@@ -203,37 +207,44 @@ def build_token_plan(dev, m, qt, cache):
     q = dev.fill_normal(dev.alloc(H * D * 2), m.F16, H * D, SEED ^ 0x701, 1.0)
     k = dev.fill_normal(dev.alloc(cache * H * D * 2), m.F16, cache * H * D, SEED ^ 0x702, 1.0)
     v = dev.fill_normal(dev.alloc(cache * H * D * 2), m.F16, cache * H * D, SEED ^ 0x703, 1.0)
-    o = dev.alloc(H * D * 2)
+    o = dev.alloc(H * D * 4)
     tok = dev.alloc(4)
     plan = m.Plan(dev)
+    plan.set_fusion(fuse)
     for layer in range(24):
         i0 = 4 * layer
         plan.add_gemv_grouped([(x_of["qkv"], m.F32, weights[i0], ys[i0], m.F32),
                                (x_of["fc1"], m.F32, weights[i0 + 2], ys[i0 + 2], m.F32)],
                               epilogues=[eps[i0], eps[i0 + 2]])
-        plan.add_attention(q, k, v, o, m.F16, 1, cache, H, D, causal=False)
-        plan.add_gemv_grouped([(x_of["dense"], m.F32, weights[i0 + 1], ys[i0 + 1], m.F32),
+        plan.add_attention(q, k, v, o, m.F32, 1, cache, H, D, causal=False)
+        plan.add_gemv_grouped([(o, m.F32, weights[i0 + 1], ys[i0 + 1], m.F32),
                                (x_of["fc2"], m.F32, weights[i0 + 3], ys[i0 + 3], m.F32)],
                               epilogues=[eps[i0 + 1], eps[i0 + 3]])
     plan.add_gemv(x_of["lm_head"], m.F32, weights[-1], ys[-1], m.F32, 1)
     plan.add_argmax(ys[-1], m.F32, 1, 51200, 51200, tok)
-    return plan, weights, {"x": x_of, "y": ys, "ep": eps, "token": tok, "q": q, "k": k, "v": v, "o": o}
+    xs = [x_of["qkv"], o, x_of["fc1"], x_of["fc2"]] * 24 + [x_of["lm_head"]]
+    return plan, weights, {"x": xs, "y": ys, "ep": eps, "token": tok, "q": q, "k": k, "v": v, "o": o}
 
 
-def decode_token(dev, m, qt, cache, steps, warmup):
+def decode_token(dev, m, qt, cache, steps, warmup, fuse=True):
     """One Phi-1.5 decode step with the path's own ops end to end (build_token_plan)."""
-    plan, weights, _ = build_token_plan(dev, m, qt, cache)
+    plan, weights, _ = build_token_plan(dev, m, qt, cache, fuse)
+    fused = plan.fused()
     plan.use_graph(True)
     ms = timed_plan(dev, plan, steps, warmup)
+    plan.check()
     plan.destroy()
     for W in weights:
         W.free()
     nbytes = (sum(gemv_bytes(qt, N, K, 1) for _, N, K in PHI_STEP)   # weights, x, y
               + 24 * 2 * cache * 32 * 64 * 2.0                        # the KV cache, fp16
               + 51200 * 4.0)                                          # logits read by the token pick
-    return {"workload": f"phi15_decode_token_{qt}_cache{cache}", "us": ms * 1e3, "tokens_per_s": 1e3 / ms,
-            "ops": 24 * 3 + 2, "epilogues": "QKV+bias, fc1+bias+GELU, dense+bias+residual, fc2+bias+residual "
-                                            "fused into the grouped GEMVs",
+    return {"workload": f"phi15_decode_token_{qt}_cache{cache}" + ("" if fuse else "_unfused"), "us": ms * 1e3,
+            "tokens_per_s": 1e3 / ms, "ops": 24 * 3 + 2, "launches": 24 * 3 + 2 - fused,
+            "attention": ("each layer's attention computed inside its {dense, fc2} launch (plan fusion)" if fused
+                          else "one launch per layer"),
+            "epilogues": "QKV+bias, fc1+bias+GELU, dense+bias+residual, fc2+bias+residual "
+                         "fused into the grouped GEMVs",
             "bytes_per_token": nbytes,
             "roofline": roofline("hbm", nbytes / ms / 1e6, "timed region (HIP events around the graph replays) "
                                  "/ tokens; bytes = weights, x and y of the 97 GEMVs, the KV cache, the logits")}
@@ -854,11 +865,12 @@ def main():
             extra[r["workload"]] = r
             log(f"[bench]   {r['workload']}: {r['ms_per_step'] * 1e3:.1f} us/step {r['gbs']:.0f} GB/s "
                 f"({100 * r['frac']:.1f}%)")
-        for qt, cache in (("q8_0", 512), ("q8_0", 2048), ("q4_0", 512)):
-            r = decode_token(dev, m, qt, cache, max(10, args.steps // 2), 3)
+        for qt, cache, fuse in (("q8_0", 512, True), ("q8_0", 512, False), ("q8_0", 2048, True),
+                                ("q4_0", 512, True)):
+            r = decode_token(dev, m, qt, cache, max(10, args.steps // 2), 3, fuse)
             extra[r["workload"]] = r
             log(f"[bench]   {r['workload']}: {r['us']:.1f} us/token ({r['tokens_per_s']:.0f} tokens/s; GEMVs, "
-                f"attention, LM head and token pick, one graph)")
+                f"attention, LM head and token pick, one graph of {r['launches']} launches)")
         r = fp32_gemv(dev, m, max(10, args.steps // 2), 3)
         extra[r["workload"]] = r
         log(f"[bench]   {r['workload']}: {r['us']:.1f} us {r['gbs']:.0f} GB/s ({100 * r['frac']:.1f}%)")

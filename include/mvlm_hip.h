@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MVLM_ABI_VERSION 2
+#define MVLM_ABI_VERSION 3
 
 /* ---- status codes ------------------------------------------------------- */
 enum mvlm_status {
@@ -361,8 +361,30 @@ int mvlm_plan_use_graph(mvlm_plan* plan, int enable);
 int mvlm_plan_run(mvlm_plan* plan, int repeats, mvlm_event** ev);
 /* One eager run in which every launch carries start/stop events on its own
  * dispatch: op_ms[i] is the execution time of launch i (the figure
- * rocprofv3 --kernel-trace reports for that dispatch). */
+ * rocprofv3 --kernel-trace reports for that dispatch); an entry carried by
+ * the next entry's launch (plan fusion) reports 0. */
 int mvlm_plan_profile(mvlm_plan* plan, float* op_ms, int capacity);
+/* Plan fusion.  No counterpart in the reference, whose decode loop launches
+ * attention_decode and then the output projection
+ * (src/models/moondream2.cpp:423-446).  A decode attention entry (seq_q == 1,
+ * F32 output, head_dim 64 or 128) followed directly by a grouped M == 1 GEMV
+ * entry (F32 x) that reads the attention output as some entries' x runs
+ * inside that GEMV's launch: its workgroups come first, and the entries that
+ * read the output wait for it after loading their weights.  The pair is
+ * fused when the GEMV entry is added and fits (its entries neither write the
+ * attention's inputs or output nor read the output except as x, weight rows
+ * of at most 4 KiB in HBM (codes only for Q8_0 / Q4_0: K <= 4096 / 8192) for
+ * the waiting entries, and those entries' workgroups cannot
+ * fill the device alone); otherwise both launch as before.  On by default;
+ * set_fusion(0) launches every entry separately (drops a captured graph).
+ * mvlm_plan_fused returns the number of fused pairs in effect.
+ * A waiting workgroup gives up after 20 ms and stores NaN;
+ * mvlm_plan_check synchronizes and returns MVLM_ERR_HIP if a fused launch of
+ * the plan gave up since the last check (and clears that launch site's
+ * counters, so later runs start clean). */
+int mvlm_plan_set_fusion(mvlm_plan* plan, int enable);
+int mvlm_plan_fused(const mvlm_plan* plan);
+int mvlm_plan_check(mvlm_plan* plan);
 
 /* ---- stream markers for host-side timing of a region ---------------------- */
 /* Records a marker on the device stream; elapsed time between two markers. */

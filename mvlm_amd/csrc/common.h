@@ -213,9 +213,32 @@ hipError_t launch_gemv_stream(hipStream_t s, const void* x, int x_dtype, const m
 // One launch for up to 8 independent problems of one weight dtype and x dtype;
 // M > 1 (quantized weights, fp32 x and y, M <= 4) streams each weight once for
 // its M rows of x.
+struct StreamAttnDesc;
 hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const* xs, int x_dtype,
                                     const mvlm_weight* const* ws, void* const* ys, const int* y_dtypes, int num_cus,
-                                    const Epilogue* eps = nullptr, int M = 1);
+                                    const Epilogue* eps = nullptr, int M = 1, const StreamAttnDesc* at = nullptr);
+// Decode attention (one query per head against seq_kv cached keys; fp16 q
+// [heads][D], K and V [seq_kv][heads][D]; fp32 output o [heads][D]) carried by
+// an M = 1 grouped launch whose problems with x == o read its output: the
+// attention runs in the launch's first workgroups, the problems reading o
+// wait for it after loading their weights (gemv_stream.hip).
+struct StreamAttnDesc {
+    const void* q = nullptr;
+    const void* k = nullptr;
+    const void* v = nullptr;
+    float* o = nullptr;
+    int heads = 0, head_dim = 0, seq_kv = 0;
+    float scale = 0.0f;
+    void* workspace = nullptr;     // stream_attn_workspace_bytes
+    void* sync = nullptr;          // SYNC_BYTES of the launch site, zeroed before its first launch
+};
+constexpr size_t SYNC_BYTES = 48 * 1024;
+constexpr size_t SYNC_ERR_OFFSET = 256;   // u32 error word of a sync area
+size_t stream_attn_workspace_bytes(int heads, int head_dim, int seq_kv, int num_cus);
+// hipSuccess when this launch can carry the attention: M = 1, fp32 x, head_dim
+// 64 or 128, and the blocks that wait fit on the device at once beside others
+hipError_t stream_attn_check(int count, const void* const* xs, int x_dtype, const mvlm_weight* const* ws,
+                             const StreamAttnDesc& at, int num_cus);
 // Skinny GEMM over up to 8 independent problems (quantized weights of one
 // dtype, fp32 X [M][K] and Y [M][N] each, 1 <= M <= 16) in one launch.
 hipError_t launch_gemm_skinny_group(hipStream_t s, int M, int count, const float* const* Xs,

@@ -127,8 +127,12 @@ __device__ __forceinline__ int x_slot(int s) { return s ^ ((s >> 4) & (SL - 1));
 // direct W-byte loads; the waves of the block take pieces of 64*W bytes in
 // turn.  With SL > 1 the 16-byte slots are permuted by x_slot.  Source reads
 // are clamped to [0, nbytes - W]: bytes landing beyond nbytes are never read,
-// and the LDS region is rounded up to whole pieces.
-template <int W, int SL, int NW>
+// and the LDS region is rounded up to whole pieces.  CPOL is the loads' cache
+// policy: 0, or kCpolDevice for data another workgroup of the same launch
+// wrote with device-scope stores (read at the device coherence point, not from
+// a possibly stale line of this XCD's L2).
+constexpr int kCpolDevice = 16;   // sc1
+template <int W, int SL, int NW, int CPOL = 0>
 __device__ __forceinline__ void stage_to_lds(uint8_t* dst, const uint8_t* __restrict__ src, int nbytes,
                                              int wave, int lane) {
     static_assert(W == 4 || W == 16, "direct load width");
@@ -136,8 +140,8 @@ __device__ __forceinline__ void stage_to_lds(uint8_t* dst, const uint8_t* __rest
         const int phys = piece * 64 * W + lane * W;
         const int logical = x_slot<SL>(phys >> 4) * 16 + (phys & 15);
         const uint8_t* from = src + min(logical, nbytes - W);
-        if constexpr (W == 16) __builtin_amdgcn_global_load_lds(from, (lds_void*)(dst + piece * 64 * W), 16, 0, 0);
-        else __builtin_amdgcn_global_load_lds(from, (lds_void*)(dst + piece * 64 * W), 4, 0, 0);
+        if constexpr (W == 16) __builtin_amdgcn_global_load_lds(from, (lds_void*)(dst + piece * 64 * W), 16, 0, CPOL);
+        else __builtin_amdgcn_global_load_lds(from, (lds_void*)(dst + piece * 64 * W), 4, 0, CPOL);
     }
 }
 

@@ -31,7 +31,9 @@
 // of each block: different rounding, same value within the fp32 tolerance.
 #include "gemv_common.h"
 
+#include <algorithm>
 #include <type_traits>
+#include <vector>
 
 namespace mvlm {
 
@@ -55,6 +57,7 @@ struct StreamProblem {
     int rows_per_block;            // block j owns rows [j*rows_per_block, (j+1)*rows_per_block) below N
     int block_begin;               // first block of this problem in the grid
     int ep_on;
+    int dep;                       // x is the output of the launch's attention (waits for it)
     Epilogue ep;                   // applied to y when ep_on
 };
 
@@ -64,10 +67,315 @@ constexpr int MAX_GROUP = 8;
 #endif
 constexpr int NWAVE = MVLM_STREAM_WAVES;   // waves per block
 
+// ---- decode attention carried by a grouped launch ----------------------------
+//
+// Phi-1.5's decode attention (one query per head against the KV cache, the
+// work of attention_decode, src/kernels/attention.cl:197-295) sits between its
+// grouped {QKV, fc1} and {dense, fc2} GEMVs.  As a launch of its own it costs
+// a kernel boundary for ~4 MB of cache reads.  Here it runs in the first
+// workgroups of the {dense, fc2} launch instead:
+//  * attention workgroup (head h, key split s) streams its keys and values
+//    (online softmax per wave, merged across waves in LDS) and leaves a
+//    partial result: unnormalised output, running max, sum of weights; the
+//    last split of a head to finish (a device-scope counter per head) merges
+//    the splits, writes o[h] and bumps the launch's done counter;
+//  * workgroups of the problems whose x is o issue their weight loads first,
+//    then wait (one lane polls) until every head is done, then stage o in
+//    LDS.
+// The counters live in a sync area of the launch site (one per fused plan
+// entry, zeroed once) and only ever grow, so no launch resets anything and
+// no atomic is awaited by every waiting workgroup (a counter that 256
+// workgroups bump serialises for ~3 us):
+//   byte 0      u64  done: heads finished over all launches; the bump that
+//                    completes a launch's heads writes go = launches so far
+//   byte 256    u32  error word
+//   byte 1024   u32  go[16], 128 bytes apart (the waiting workgroups poll
+//                    go[c % 16], spreading the polls over 16 lines)
+//   byte 4096   u64  head[h], 64 bytes apart: splits of head h finished;
+//                    the bump reaching a multiple of splits merges
+//   byte 16384  u32  seen[c]: launches waiting workgroup c has waited
+//                    through (its own word: it waits for go >= seen + 1)
+// Launches of one site run one after another on the stream, so each
+// launch's counts are whole multiples when the next begins.
+// Only the waiting workgroups wait, and only on workgroups that never wait,
+// so the launch completes as long as the waiting ones cannot fill the device
+// by themselves (checked on the host against the kernel's occupancy).  A
+// wait still gives up after 20 ms: the workgroup then stores NaN instead of
+// its outputs and sets the error word (read by mvlm_plan_check, which then
+// clears the area).
+// Data crossing workgroups (partials, o) moves with device-scope (sc1) stores
+// and loads, and every such store is complete (s_waitcnt vmcnt(0)) before
+// the counter that publishes it is bumped.
+constexpr int SYNC_DONE_B = 0, SYNC_ERR_B = (int)SYNC_ERR_OFFSET, SYNC_GO_B = 1024, SYNC_HEAD_B = 4096, SYNC_SEEN_B = 16384;
+constexpr int SYNC_GO_N = 16;
+constexpr int ATTN_MAX_HEADS = (SYNC_SEEN_B - SYNC_HEAD_B) / 64;
+constexpr int ATTN_MAX_CONSUMERS = (int)(SYNC_BYTES - SYNC_SEEN_B) / 4;
+constexpr int ATTN_NL = 2;                     // key (and value) loads per lane and iteration
+constexpr int ATTN_MAX_SPLITS = 32;
+constexpr uint64_t ATTN_TIMEOUT = 2000000;     // s_memrealtime ticks (100 MHz): 20 ms
+
+struct StreamAttn {
+    const uint16_t* q;         // [heads][D]
+    const uint16_t* k;         // [seq_kv][heads][D]
+    const uint16_t* v;
+    float* o;                  // [heads][D]
+    float* part_o;             // [heads][splits][D] unnormalised outputs of the splits
+    float* part_ml;            // [heads][splits][2] running max (exp2 domain) and sum of weights
+    uint8_t* sync;             // the site's sync area
+    int heads, D, seq_kv, splits, keys_per_split, blocks, consumers;
+    float scale_log2;          // scale * log2(e)
+};
+
 struct StreamGroup {
     StreamProblem p[MAX_GROUP];
     int count;
+    StreamAttn at;             // used by the launches that carry attention
 };
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void* p, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ void stores_complete() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+template <typename T>
+__device__ __forceinline__ T* sync_word(const StreamAttn& a, int byte) {
+    return reinterpret_cast<T*>(a.sync + byte);
+}
+__device__ __forceinline__ uint64_t sync_add64(uint64_t* p) {
+    return __hip_atomic_fetch_add(p, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void sync_store(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t sync_load(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// lane 0's value of a 64-bit counter result, in every lane
+__device__ __forceinline__ uint64_t first_lane64(uint64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Head h's o is stored and complete: count it; the count completing a
+// launch's heads publishes the launch number in every go line.
+__device__ __forceinline__ void attn_head_done(const StreamAttn& a, int lane) {
+    uint64_t old = 0;
+    if (lane == 0) old = sync_add64(sync_word<uint64_t>(a, SYNC_DONE_B));
+    const uint64_t n = first_lane64(old) + 1;
+    if (n % (uint64_t)a.heads == 0 && lane < SYNC_GO_N)
+        sync_store(sync_word<uint32_t>(a, SYNC_GO_B + 128 * lane), (uint32_t)(n / (uint64_t)a.heads));
+}
+
+// One attention workgroup: keys [k0, k1) of head h.  Wave w takes keys
+// k0 + 16w + 128i .. (D = 64; 8 lanes of 16 bytes per key, ATTN_NL keys per
+// lane and iteration), scores in the exp2 domain.
+template <int D>
+__device__ void attn_decode_block(const StreamAttn& a, float* lds, int wave, int lane) {
+    constexpr int LPK = D / 8;                 // lanes per key
+    constexpr int KPI = 64 / LPK;              // keys per wave-wide load
+    constexpr int KPW = ATTN_NL * KPI;         // keys per wave and iteration
+    constexpr int DPL = D / 64;                // output dims per lane in the merges
+    const int h = (int)blockIdx.x / a.splits, sp = (int)blockIdx.x - h * a.splits;
+    const int k0 = sp * a.keys_per_split, k1 = min(k0 + a.keys_per_split, a.seq_kv);
+    const int sub = lane % LPK, kl = lane / LPK;
+    const int64_t key_stride = (int64_t)a.heads * D;
+    const int col = h * D + sub * 8;
+    float qf[8];
+    {
+        const u32x4 u = *reinterpret_cast<const u32x4*>(a.q + col);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            qf[2 * j] = f16_bits_to_f32((uint16_t)(u[j] & 0xFFFFu)) * a.scale_log2;
+            qf[2 * j + 1] = f16_bits_to_f32((uint16_t)(u[j] >> 16)) * a.scale_log2;
+        }
+    }
+    float m = -INFINITY, l = 0.0f, o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+    for (int base = k0 + wave * KPW; base < k1; base += NWAVE * KPW) {
+        u32x4 kr[ATTN_NL], vr[ATTN_NL];
+        int key[ATTN_NL];
+#pragma unroll
+        for (int j = 0; j < ATTN_NL; ++j) {
+            key[j] = base + j * KPI + kl;
+            const int64_t r = min(key[j], k1 - 1);
+            kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.k + r * key_stride + col));
+        }
+#pragma unroll
+        for (int j = 0; j < ATTN_NL; ++j) {
+            const int64_t r = min(key[j], k1 - 1);
+            vr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.v + r * key_stride + col));
+        }
+        float s[ATTN_NL], mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < ATTN_NL; ++j) {
+            float d = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                d = __builtin_fmaf(qf[2 * e], f16_bits_to_f32((uint16_t)(kr[j][e] & 0xFFFFu)), d);
+                d = __builtin_fmaf(qf[2 * e + 1], f16_bits_to_f32((uint16_t)(kr[j][e] >> 16)), d);
+            }
+#pragma unroll
+            for (int off = 1; off < LPK; off <<= 1) d += __shfl_xor(d, off);
+            s[j] = key[j] < k1 ? d : -INFINITY;
+            mx = fmaxf(mx, s[j]);
+        }
+#pragma unroll
+        for (int off = LPK; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        const float mn = fmaxf(m, mx);               // finite: key `base` is below k1
+        const float alpha = __builtin_amdgcn_exp2f(m - mn);
+        l *= alpha;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] *= alpha;
+#pragma unroll
+        for (int j = 0; j < ATTN_NL; ++j) {
+            const float p = __builtin_amdgcn_exp2f(s[j] - mn);
+            l += p;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                o[2 * e] = __builtin_fmaf(p, f16_bits_to_f32((uint16_t)(vr[j][e] & 0xFFFFu)), o[2 * e]);
+                o[2 * e + 1] = __builtin_fmaf(p, f16_bits_to_f32((uint16_t)(vr[j][e] >> 16)), o[2 * e + 1]);
+            }
+        }
+        m = mn;
+    }
+    // sums over the wave's key groups: lanes of one sub end with the wave's totals
+#pragma unroll
+    for (int off = LPK; off < 64; off <<= 1) {
+        l += __shfl_xor(l, off);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] += __shfl_xor(o[e], off);
+    }
+    float* mine = lds + wave * (D + 2);
+    if (lane < LPK) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mine[lane * 8 + e] = o[e];
+    }
+    if (lane == 0) {
+        mine[D] = m;
+        mine[D + 1] = l;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    // merge the waves (a wave without keys has m = -inf: weight 0); lane owns
+    // dims lane + 64 t
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) M = fmaxf(M, lds[w * (D + 2) + D]);
+    float L = 0.0f, acc[DPL];
+#pragma unroll
+    for (int t = 0; t < DPL; ++t) acc[t] = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) {
+        const float f = __builtin_amdgcn_exp2f(lds[w * (D + 2) + D] - M);
+        L = __builtin_fmaf(lds[w * (D + 2) + D + 1], f, L);
+#pragma unroll
+        for (int t = 0; t < DPL; ++t) acc[t] = __builtin_fmaf(lds[w * (D + 2) + lane + 64 * t], f, acc[t]);
+    }
+    const __amdgpu_buffer_rsrc_t orr = dev_rsrc(a.o + h * D, D * 4);
+    if (a.splits == 1) {
+#pragma unroll
+        for (int t = 0; t < DPL; ++t)
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc[t] / L), orr, (lane + 64 * t) * 4, 0,
+                                                 kCpolDevice);
+        stores_complete();
+        attn_head_done(a, lane);
+        return;
+    }
+    const __amdgpu_buffer_rsrc_t por = dev_rsrc(a.part_o + (int64_t)h * a.splits * D, a.splits * D * 4);
+    const __amdgpu_buffer_rsrc_t pmr = dev_rsrc(a.part_ml + (int64_t)h * a.splits * 2, a.splits * 8);
+#pragma unroll
+    for (int t = 0; t < DPL; ++t)
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc[t]), por, (sp * D + lane + 64 * t) * 4,
+                                             0, kCpolDevice);
+    if (lane == 0) {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, M), pmr, sp * 8, 0, kCpolDevice);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, L), pmr, sp * 8 + 4, 0, kCpolDevice);
+    }
+    stores_complete();
+    uint64_t arrived = 0;
+    if (lane == 0) arrived = sync_add64(sync_word<uint64_t>(a, SYNC_HEAD_B + 64 * h));
+    if ((first_lane64(arrived) + 1) % (uint64_t)a.splits != 0) return;
+    // the last split of head h merges all of them.  Lane s < splits reads
+    // split s's max and sum; the outputs come in as 16-byte pieces, 256
+    // floats per wave-wide load (lane j: dims 4j % D .. + 3 of split
+    // (256 i + 4 j) / D), four loads at a time, loads past the splits
+    // reading zeros.
+    constexpr int NB = 4;
+    const int ni = (a.splits * D + 255) / 256;
+    u32x4 pv[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+        pv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(por, (256 * i + 4 * lane) * 4, 0,
+                                                                               kCpolDevice));
+    const float ms = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pmr, lane * 8, 0, kCpolDevice));
+    const float ls = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pmr, lane * 8 + 4, 0, kCpolDevice));
+    float Mh = lane < a.splits ? ms : -INFINITY;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) Mh = fmaxf(Mh, __shfl_xor(Mh, off));
+    const float fs = lane < a.splits ? __builtin_amdgcn_exp2f(ms - Mh) : 0.0f;
+    float Lh = lane < a.splits ? ls * fs : 0.0f;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) Lh += __shfl_xor(Lh, off);
+    float r4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i0 = 0; i0 < ni; i0 += NB) {
+        if (i0 > 0) {
+#pragma unroll
+            for (int i = 0; i < NB; ++i)
+                pv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      por, (256 * (i0 + i) + 4 * lane) * 4, 0, kCpolDevice));
+        }
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const int split = min((256 * (i0 + i) + 4 * lane) / D, ATTN_MAX_SPLITS - 1);   // zeros past the splits
+            const float f = __shfl(fs, split);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r4[e] = __builtin_fmaf(__uint_as_float(pv[i][e]), f, r4[e]);
+        }
+    }
+    // lanes holding the same dims: j, j + D/4, ... (D = 64: 4 of them, D = 128: 2)
+#pragma unroll
+    for (int off = D / 4; off < 64; off <<= 1)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r4[e] += __shfl_xor(r4[e], off);
+    if (lane < D / 4) {
+        u32x4 out;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[e] = __builtin_bit_cast(uint32_t, r4[e] / Lh);
+        __builtin_amdgcn_raw_buffer_store_b128(out, orr, lane * 16, 0, kCpolDevice);
+    }
+    stores_complete();
+    attn_head_done(a, lane);
+}
+
+// Waiting workgroup c (of the launch's consumers): wait until this launch's
+// heads are all done, i.e. go >= seen[c] + 1, and count the launch in
+// seen[c] (lane 0 of wave 0).  Returns false when the wait gave up (the
+// workgroup then stores NaN).
+__device__ __forceinline__ bool attn_wait(const StreamAttn& a, int wave, int lane, uint32_t* flag) {
+    if (wave == 0 && lane == 0) {
+        const int c = (int)blockIdx.x - (int)gridDim.x + a.consumers;
+        uint32_t* seen = sync_word<uint32_t>(a, SYNC_SEEN_B + 4 * c);
+        const uint32_t want = sync_load(seen) + 1;
+        const uint32_t* go = sync_word<uint32_t>(a, SYNC_GO_B + 128 * (c % SYNC_GO_N));
+        uint32_t ok = 1;
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        while ((int32_t)(sync_load(go) - want) < 0) {
+            if (__builtin_amdgcn_s_memrealtime() - t0 > ATTN_TIMEOUT) {
+                ok = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        sync_store(seen, want);
+        if (!ok) sync_store(sync_word<uint32_t>(a, SYNC_ERR_B), 1u);
+        *flag = ok;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    return *flag != 0;
+}
 
 // Work shape of one wave by row length in 1 KiB chunks: R rows x CW chunks,
 // the row split over SPLIT waves when it is longer than CW chunks.  A wave
@@ -80,6 +388,10 @@ struct Shape { int max_chunks, R, CW, SPLIT; };
 constexpr Shape kShapes[] = {{1, 4, 1, 1}, {2, 2, 2, 1}, {4, 1, 4, 1}, {8, 1, 4, 2}, {16, 1, 8, 2}, {8, 2, 4, 2},
                              {2, 1, 2, 1}};
 constexpr int kNumShapes = 7, kByLength = 5, kBatchLong = 5, kFewRows2 = 6;
+// Shapes a problem that waits for the launch's attention may take: rows of at
+// most 4 KiB in HBM (with longer rows the registers holding the code loads
+// during the wait push the kernel past its register budget).
+constexpr bool kDepShape[] = {true, true, true, false, false, false, true};
 static_assert(sizeof(kShapes) / sizeof(kShapes[0]) == kNumShapes, "one kernel case per shape");
 
 // The rows [row0, row0 + R) of one wave (those below the block's end rb1),
@@ -87,10 +399,12 @@ static_assert(sizeof(kShapes) / sizeof(kShapes[0]) == kNumShapes, "one kernel ca
 // LDS byte m * x_stride; rows of x at or past M repeat row M-1 and are not
 // stored).  x and the scales are already being staged into LDS (staging loads
 // were issued before these and complete first).
-template <class F, typename XT, int MX, int R, int CW, int SPLIT>
+// With DEP, x is the launch's attention output and not staged yet: the wave
+// waits for the attention after issuing its code loads, then stages x.
+template <class F, typename XT, int MX, int R, int CW, int SPLIT, bool DEP>
 __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int rb1, int64_t s_base, int x_stride,
-                                            int x_region, const uint8_t* lds, float (*part)[4 * MX], int wave,
-                                            int lane) {
+                                            int x_region, uint8_t* lds, float (*part)[4 * MX], int wave,
+                                            int lane, const StreamAttn& at, uint32_t* wait_ok) {
     constexpr int WPL = F::WPL;
     constexpr int XB = WPL * (int)sizeof(XT);        // x bytes per lane per chunk
     constexpr int SL = XB >= 16 ? XB / 16 : 1;       // 16-byte LDS slots per lane per chunk
@@ -138,7 +452,15 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
     }
 
     // staging done for every wave -> x and scales from LDS, chunk by chunk
-    wait_vmcnt<R * CW>();
+    bool ok = true;
+    if constexpr (DEP) {
+        ok = attn_wait(at, wave, lane, wait_ok);
+        stage_to_lds<(XB >= 16 ? 16 : 4), SL, NWAVE, kCpolDevice>(lds, (const uint8_t*)P.x, K * (int)sizeof(XT),
+                                                                    wave, lane);
+        wait_vmcnt<0>();
+    } else {
+        wait_vmcnt<R * CW>();
+    }
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     // Q4_0: the block sums of each row of x (the -8 offset's term, sxl[m][b]),
@@ -241,6 +563,7 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
     // y[m][row] (and the epilogue's mul / residual [m][row], bias [row]),
     // the NV outputs of a wave stored by NV lanes at once
     auto store_row = [&](int row, int m, float v) {
+        if constexpr (DEP) v = ok ? v : __builtin_nanf("");
         if constexpr (MX == 1) {
             store_out(P.y, row, P.ep_on ? apply_epilogue(P.ep, v, row, row) : v, P.y_dtype);
         } else {
@@ -270,22 +593,33 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
 // registers.  Issue order: x and scale staging, then every code load, then
 // the wait for the staging alone (vmcnt counts in issue order), the block
 // barrier, the LDS reads, and the wait for the codes.
-template <class F, typename XT, int MX>
+// ATTN: the launch's first at.blocks workgroups compute the decode attention
+// (attn_decode_block); the problems marked dep read its output as x.
+template <class F, typename XT, int MX, bool ATTN>
 __global__ __launch_bounds__(64 * NWAVE, MX == 1 ? F::MIN_WAVES : F::MIN_WAVES_BATCH) void gemv_stream_kernel(
     const StreamGroup g) {
     constexpr int XB = F::WPL * (int)sizeof(XT);
     constexpr int SL = XB >= 16 ? XB / 16 : 1;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ float part[NWAVE][4 * MX];
+    __shared__ uint32_t wait_ok;
 
+    // the wave index is uniform: keep it in a scalar register so the staging
+    // loops and row offsets are scalar code
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if constexpr (ATTN) {
+        if ((int)blockIdx.x < g.at.blocks) {
+            if (g.at.D == 64) attn_decode_block<64>(g.at, reinterpret_cast<float*>(lds), wave, lane);
+            else attn_decode_block<128>(g.at, reinterpret_cast<float*>(lds), wave, lane);
+            return;
+        }
+    }
     int pi = 0;
 #pragma unroll
     for (int i = 1; i < MAX_GROUP; ++i)
         if (i < g.count && (int)blockIdx.x >= g.p[i].block_begin) pi = i;
     const StreamProblem& P = g.p[pi];
-    // the wave index is uniform: keep it in a scalar register so the staging
-    // loops and row offsets are scalar code
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool dep = ATTN && P.dep;
     const int N = P.N, K = P.K, nb = K >> 5;
     const int rb0 = ((int)blockIdx.x - P.block_begin) * P.rows_per_block;
     const int rb1 = min(rb0 + P.rows_per_block, N);
@@ -295,11 +629,13 @@ __global__ __launch_bounds__(64 * NWAVE, MX == 1 ? F::MIN_WAVES : F::MIN_WAVES_B
     const int x_bytes = K * (int)sizeof(XT);
     const int x_stride = (x_bytes + 1023) & ~1023;
     const int x_region = MX * x_stride;
+    if (!dep) {
 #pragma unroll
-    for (int m = 0; m < MX; ++m)
-        stage_to_lds<(XB >= 16 ? 16 : 4), SL, NWAVE>(lds + m * x_stride,
-                                                    (const uint8_t*)P.x + (m == 0 ? 0 : (int64_t)min(m, P.M - 1) * x_bytes),
-                                                    x_bytes, wave, lane);
+        for (int m = 0; m < MX; ++m)
+            stage_to_lds<(XB >= 16 ? 16 : 4), SL, NWAVE>(
+                lds + m * x_stride, (const uint8_t*)P.x + (m == 0 ? 0 : (int64_t)min(m, P.M - 1) * x_bytes), x_bytes,
+                wave, lane);
+    }
     int64_t s_base = 0;                               // global byte offset of the first staged scale byte
     if constexpr (F::QUANT) {
         const int64_t s_begin = (int64_t)rb0 * (nb * 2);
@@ -310,24 +646,28 @@ __global__ __launch_bounds__(64 * NWAVE, MX == 1 ? F::MIN_WAVES : F::MIN_WAVES_B
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    switch (P.shape) {   // uniform over the block
-#define MVLM_SHAPE_CASE(i)                                                                               \
-    case i:                                                                                              \
-        stream_rows<F, XT, MX, kShapes[i].R, kShapes[i].CW, kShapes[i].SPLIT>(P, rb0, rb1, s_base, x_stride, \
-                                                                               x_region, lds, part, wave, lane); \
-        break;
-        MVLM_SHAPE_CASE(0) MVLM_SHAPE_CASE(1) MVLM_SHAPE_CASE(2) MVLM_SHAPE_CASE(3) MVLM_SHAPE_CASE(4)
-#undef MVLM_SHAPE_CASE
-    case kFewRows2:
-        if constexpr (MX == 1)
-            stream_rows<F, XT, MX, kShapes[kFewRows2].R, kShapes[kFewRows2].CW, kShapes[kFewRows2].SPLIT>(
-                P, rb0, rb1, s_base, x_stride, x_region, lds, part, wave, lane);
-        break;
-    case kBatchLong:
-        if constexpr (MX > 1)
-            stream_rows<F, XT, MX, kShapes[kBatchLong].R, kShapes[kBatchLong].CW, kShapes[kBatchLong].SPLIT>(
-                P, rb0, rb1, s_base, x_stride, x_region, lds, part, wave, lane);
-        break;
+    auto rows = [&](auto shape) {   // uniform over the block
+        constexpr int si = decltype(shape)::value;
+        constexpr Shape S = kShapes[si];
+        if (ATTN && kDepShape[si] && dep)
+            stream_rows<F, XT, MX, S.R, S.CW, S.SPLIT, ATTN>(P, rb0, rb1, s_base, x_stride, x_region, lds, part, wave,
+                                                             lane, g.at, &wait_ok);
+        else
+            stream_rows<F, XT, MX, S.R, S.CW, S.SPLIT, false>(P, rb0, rb1, s_base, x_stride, x_region, lds, part, wave,
+                                                              lane, g.at, &wait_ok);
+    };
+    switch (P.shape) {
+        case 0: rows(std::integral_constant<int, 0>{}); break;
+        case 1: rows(std::integral_constant<int, 1>{}); break;
+        case 2: rows(std::integral_constant<int, 2>{}); break;
+        case 3: rows(std::integral_constant<int, 3>{}); break;
+        case 4: rows(std::integral_constant<int, 4>{}); break;
+        case kFewRows2:
+            if constexpr (MX == 1) rows(std::integral_constant<int, kFewRows2>{});
+            break;
+        case kBatchLong:
+            if constexpr (MX > 1) rows(std::integral_constant<int, kBatchLong>{});
+            break;
     }
 }
 
@@ -390,21 +730,26 @@ int stream_max_group() { return MAX_GROUP; }
 // x, so x traffic grows with the block count, and part-filled blocks idle
 // waves.  Computing block bounds by division, even once per block, also cost
 // ~0.2 us per launch.)
+// The attention's workgroups come first; the problems' blocks follow.
 static unsigned partition(StreamGroup& g) {
-    unsigned begin = 0;
+    unsigned begin = (unsigned)g.at.blocks;
+    g.at.consumers = 0;
     for (int i = 0; i < g.count; ++i) {
         StreamProblem& p = g.p[i];
         p.rows_per_block = rows_per_block(p.shape);
         p.block_begin = (int)begin;
-        begin += (unsigned)((p.N + p.rows_per_block - 1) / p.rows_per_block);
+        const unsigned nblk = (unsigned)((p.N + p.rows_per_block - 1) / p.rows_per_block);
+        begin += nblk;
+        if (p.dep) g.at.consumers += (int)nblk;
     }
     return begin;
 }
 
-template <class F, typename XT, int MX = 1>
+template <class F, typename XT, int MX = 1, bool ATTN = false>
 static hipError_t launch_group(hipStream_t s, StreamGroup& g, size_t lds) {
-    auto kernel = gemv_stream_kernel<F, XT, MX>;
-    if (const hipError_t e = allow_dynamic_lds<gemv_stream_kernel<F, XT, MX>>((int)STREAM_LDS_MAX); e != hipSuccess)
+    auto kernel = gemv_stream_kernel<F, XT, MX, ATTN>;
+    if (const hipError_t e = allow_dynamic_lds<gemv_stream_kernel<F, XT, MX, ATTN>>((int)STREAM_LDS_MAX);
+        e != hipSuccess)
         return e;
     const unsigned blocks = partition(g);
     launch_kernel(kernel, dim3(blocks), dim3(64 * NWAVE), (uint32_t)lds, s, g);
@@ -421,18 +766,112 @@ static hipError_t launch_group_x(hipStream_t s, int x_dtype, StreamGroup& g, siz
     }
 }
 
-// All problems share the weight dtype and x dtype (checked by the caller).
-// M > 1 (2..4 rows of fp32 x per problem, quantized weights) uses the
-// batched-x kernel.
-hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const* xs, int x_dtype,
-                                    const mvlm_weight* const* ws, void* const* ys, const int* y_dtypes, int num_cus,
-                                    const Epilogue* eps, int M) {
-    if (count < 1 || count > MAX_GROUP || M < 1 || M > 4) return hipErrorInvalidValue;
+// Key splits of the carried attention: enough workgroups to spread the cache
+// reads over the device (heads * splits ~ CUs), each split a whole number of
+// workgroup iterations (NWAVE waves x ATTN_NL loads x keys per load).
+static void attn_split(int heads, int D, int seq_kv, int num_cus, int* splits, int* keys_per_split) {
+    const int kb = NWAVE * ATTN_NL * (64 / (D / 8));
+    const int want = std::max(1, (num_cus + heads - 1) / heads);
+    const int s = std::max(1, std::min(std::min((seq_kv + kb - 1) / kb, want), ATTN_MAX_SPLITS));
+    const int k = ((seq_kv + s - 1) / s + kb - 1) / kb * kb;
+    *keys_per_split = k;
+    *splits = (seq_kv + k - 1) / k;
+}
+
+size_t stream_attn_workspace_bytes(int heads, int head_dim, int seq_kv, int num_cus) {
+    if (heads < 1 || (head_dim != 64 && head_dim != 128) || seq_kv < 1) return 0;
+    int splits = 1, kps = 0;
+    attn_split(heads, head_dim, seq_kv, num_cus > 0 ? num_cus : 256, &splits, &kps);
+    return ((size_t)heads * splits * head_dim * 4 + 15) / 16 * 16 + (size_t)heads * splits * 8;
+}
+
+// Fills g.at and moves the problems that read o to the end of the group
+// (marked dep).  False when the launch cannot carry the attention.
+static bool attach_attention(StreamGroup& g, const StreamAttnDesc& d, int x_dtype, int M, int num_cus,
+                             size_t& lds) {
+    if (M != 1 || x_dtype != MVLM_F32 || (d.head_dim != 64 && d.head_dim != 128) || d.heads < 1 ||
+        d.heads > ATTN_MAX_HEADS || d.seq_kv < 1 || !d.q || !d.k || !d.v || !d.o || !d.sync || !d.workspace)
+        return false;
+    if ((int64_t)d.seq_kv * d.heads * d.head_dim * 2 > (int64_t)1 << 31) return false;
+    StreamAttn& a = g.at;
+    a.q = (const uint16_t*)d.q;
+    a.k = (const uint16_t*)d.k;
+    a.v = (const uint16_t*)d.v;
+    a.o = d.o;
+    a.sync = (uint8_t*)d.sync;
+    a.heads = d.heads;
+    a.D = d.head_dim;
+    a.seq_kv = d.seq_kv;
+    attn_split(d.heads, d.head_dim, d.seq_kv, num_cus, &a.splits, &a.keys_per_split);
+    a.part_o = (float*)d.workspace;
+    a.part_ml = a.part_o + ((size_t)d.heads * a.splits * d.head_dim + 3) / 4 * 4;
+    a.blocks = d.heads * a.splits;
+    a.scale_log2 = d.scale * 1.4426950408889634f;
+    StreamProblem sorted[MAX_GROUP];
+    int n = 0;
+    for (int pass = 0; pass < 2; ++pass)
+        for (int i = 0; i < g.count; ++i)
+            if ((g.p[i].x == (const void*)d.o) == (pass == 1)) {
+                sorted[n] = g.p[i];
+                sorted[n++].dep = pass;
+            }
+    if (sorted[g.count - 1].dep == 0) return false;   // nothing reads o
+    for (int i = 0; i < g.count; ++i) {
+        if (sorted[i].dep && !kDepShape[sorted[i].shape]) return false;
+        g.p[i] = sorted[i];
+    }
+    lds = std::max(lds, (size_t)NWAVE * (d.head_dim + 2) * 4);
+    return true;
+}
+
+template <class F>
+static hipError_t attn_capacity(StreamGroup& g, size_t lds, int num_cus) {
+    int per_cu = 0;
+    if (const hipError_t e = allow_dynamic_lds<gemv_stream_kernel<F, float, 1, true>>((int)STREAM_LDS_MAX);
+        e != hipSuccess)
+        return e;
+    if (const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, gemv_stream_kernel<F, float, 1, true>, 64 * NWAVE, lds);
+        e != hipSuccess)
+        return e;
+    partition(g);
+    return g.at.consumers < per_cu * num_cus && g.at.consumers <= ATTN_MAX_CONSUMERS ? hipSuccess
+                                                                                   : hipErrorInvalidConfiguration;
+}
+
+static hipError_t build_group(StreamGroup& g, size_t& lds, int count, const void* const* xs, int x_dtype,
+                              const mvlm_weight* const* ws, void* const* ys, const int* y_dtypes, int num_cus,
+                              const Epilogue* eps, int M);
+
+hipError_t stream_attn_check(int count, const void* const* xs, int x_dtype, const mvlm_weight* const* ws,
+                             const StreamAttnDesc& at, int num_cus) {
     StreamGroup g{};
+    size_t lds = 0;
+    std::vector<void*> ys(count > 0 ? count : 1, nullptr);
+    std::vector<int> yd(count > 0 ? count : 1, MVLM_F32);
+    if (const hipError_t e = build_group(g, lds, count, xs, x_dtype, ws, ys.data(), yd.data(), num_cus, nullptr, 1);
+        e != hipSuccess)
+        return e;
+    if (!attach_attention(g, at, x_dtype, 1, num_cus, lds)) return hipErrorInvalidValue;
+    switch (ws[0]->dtype) {
+        case MVLM_Q8_0: return attn_capacity<Q8Fmt>(g, lds, num_cus);
+        case MVLM_Q4_0: return attn_capacity<Q4Fmt>(g, lds, num_cus);
+        case MVLM_F32: return attn_capacity<DenseFmt<float>>(g, lds, num_cus);
+        case MVLM_F16: return attn_capacity<DenseFmt<__half>>(g, lds, num_cus);
+        case MVLM_BF16: return attn_capacity<DenseFmt<__hip_bfloat16>>(g, lds, num_cus);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// The launch's problems (validated by the caller) and its LDS bytes.
+static hipError_t build_group(StreamGroup& g, size_t& lds, int count, const void* const* xs, int x_dtype,
+                              const mvlm_weight* const* ws, void* const* ys, const int* y_dtypes, int num_cus,
+                              const Epilogue* eps, int M) {
+    if (count < 1 || count > MAX_GROUP || M < 1 || M > 4) return hipErrorInvalidValue;
     g.count = count;
     const int dtype = ws[0]->dtype;
     if (M > 1 && (!is_quant(dtype) || x_dtype != MVLM_F32)) return hipErrorInvalidValue;
-    size_t lds = 0;
+    lds = 0;
     for (int i = 0; i < count; ++i) {
         const mvlm_weight* w = ws[i];
         StreamProblem& p = g.p[i];
@@ -454,7 +893,34 @@ hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const*
         const size_t b = stream_lds_bytes(w, x_dtype, p.shape, batch_mx(M));
         lds = b > lds ? b : lds;
     }
-    if (lds > STREAM_LDS_MAX) return hipErrorInvalidValue;
+    return lds > STREAM_LDS_MAX ? hipErrorInvalidValue : hipSuccess;
+}
+
+// All problems share the weight dtype and x dtype (checked by the caller).
+// M > 1 (2..4 rows of fp32 x per problem, quantized weights) uses the
+// batched-x kernel.  `at` (M = 1, fp32 x): the launch also computes that
+// decode attention, whose output o is the x of some of the problems
+// (stream_attn_check has accepted the combination).
+hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const* xs, int x_dtype,
+                                    const mvlm_weight* const* ws, void* const* ys, const int* y_dtypes, int num_cus,
+                                    const Epilogue* eps, int M, const StreamAttnDesc* at) {
+    StreamGroup g{};
+    size_t lds = 0;
+    if (const hipError_t e = build_group(g, lds, count, xs, x_dtype, ws, ys, y_dtypes, num_cus, eps, M);
+        e != hipSuccess)
+        return e;
+    const int dtype = ws[0]->dtype;
+    if (at) {
+        if (!attach_attention(g, *at, x_dtype, M, num_cus > 0 ? num_cus : 256, lds)) return hipErrorInvalidValue;
+        switch (dtype) {
+            case MVLM_Q8_0: return launch_group<Q8Fmt, float, 1, true>(s, g, lds);
+            case MVLM_Q4_0: return launch_group<Q4Fmt, float, 1, true>(s, g, lds);
+            case MVLM_F32: return launch_group<DenseFmt<float>, float, 1, true>(s, g, lds);
+            case MVLM_F16: return launch_group<DenseFmt<__half>, float, 1, true>(s, g, lds);
+            case MVLM_BF16: return launch_group<DenseFmt<__hip_bfloat16>, float, 1, true>(s, g, lds);
+            default: return hipErrorInvalidValue;
+        }
+    }
     if (M == 2) return dtype == MVLM_Q8_0 ? launch_group<Q8Fmt, float, 2>(s, g, lds) : launch_group<Q4Fmt, float, 2>(s, g, lds);
     if (M > 2) return dtype == MVLM_Q8_0 ? launch_group<Q8Fmt, float, 4>(s, g, lds) : launch_group<Q4Fmt, float, 4>(s, g, lds);
     switch (dtype) {

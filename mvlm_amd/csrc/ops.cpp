@@ -43,6 +43,10 @@ struct Op {
     float scale = 0.0f;
     void* workspace = nullptr;    // attention key splits, GEMM K splits
     size_t workspace_bytes = 0;
+    // grouped GEMV of a plan that can also compute the decode attention added
+    // just before it (whose output some entries read as x): plan fusion
+    bool attn_fusable = false;
+    StreamAttnDesc attn;
 };
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -308,10 +312,11 @@ int make_gemv_group(mvlm_device* dev, int M, int count, const mvlm_gemv_desc* de
 }
 
 // M > 1: the streaming kernel while every entry fits it (M <= 4), else the
-// matrix-core skinny kernel.
-static hipError_t launch_group_op(hipStream_t s, const Op& op) {
+// matrix-core skinny kernel.  with_attn: the launch also computes op.attn.
+static hipError_t launch_group_op(hipStream_t s, const Op& op, bool with_attn) {
     if (op.M == 1)
-        return launch_gemv_stream_group(s, op.gcount, op.gx, op.a_dtype, op.gw, op.gy, op.gyd, op.num_cus, op.gep);
+        return launch_gemv_stream_group(s, op.gcount, op.gx, op.a_dtype, op.gw, op.gy, op.gyd, op.num_cus, op.gep, 1,
+                                        with_attn ? &op.attn : nullptr);
     bool stream = op.M <= 4;
     for (int i = 0; i < op.gcount && stream; ++i) stream = stream_supported(op.gw[i], op.M);
     if (stream)
@@ -336,10 +341,10 @@ int make_group_epilogues(mvlm_device* dev, const mvlm_epilogue* eps, const char*
     return MVLM_OK;
 }
 
-hipError_t enqueue_op(hipStream_t s, const Op& op) {
+hipError_t enqueue_op(hipStream_t s, const Op& op, bool with_attn = false) {
     switch (op.kind) {
         case OP_GEMV_GROUP:
-            return launch_group_op(s, op);
+            return launch_group_op(s, op, with_attn);
         case OP_GEMM_NAIVE:
             return launch_gemm_naive(s, (const uint16_t*)op.a, (const uint16_t*)op.b, (uint16_t*)op.c, op.M, op.N, op.K);
         case OP_GEMM_TILED:
@@ -557,6 +562,8 @@ extern "C" int mvlm_argmax(mvlm_device* dev, const mvlm_buffer* x, int dtype, in
 struct mvlm_plan {
     mvlm_device* dev = nullptr;
     std::vector<Op> ops;
+    bool fuse = true;             // mvlm_plan_set_fusion
+    std::vector<void*> sync_areas;   // of the fusable entries (SYNC_BYTES each)
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
 };
@@ -581,14 +588,82 @@ extern "C" int mvlm_plan_create(mvlm_device* dev, mvlm_plan** out) {
 extern "C" int mvlm_plan_destroy(mvlm_plan* plan) {
     REQUIRE(plan, "mvlm_plan_destroy: plan is null");
     drop_graph(plan);
+    if (!plan->sync_areas.empty()) {
+        (void)hipSetDevice(plan->dev->ordinal);
+        (void)hipStreamSynchronize(plan->dev->stream);
+        for (void* p : plan->sync_areas) (void)hipFree(p);
+    }
     delete plan;
     return MVLM_OK;
 }
 
 extern "C" int mvlm_plan_size(const mvlm_plan* plan) { return plan ? (int)plan->ops.size() : MVLM_ERR_INVALID_ARG; }
 
-static int plan_push(mvlm_plan* plan, const Op& op) {
+static bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
+    const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+    return a && b && an && bn && x < y + bn && y < x + an;
+}
+
+// A grouped M = 1 GEMV pushed right after a decode attention (one query,
+// fp32 output, head_dim 64 or 128) that some entries read as x can carry that
+// attention in its own launch.  The entries must not write the attention's
+// inputs or output, nor read its output other than as x, and the launch must
+// fit the fused kernel (stream_attn_check).  Marks op and gives it the
+// attention's description; the plan then skips the attention launch while
+// fusion is on.
+static void mark_fusable(mvlm_plan* plan, Op& op) {
+    if (op.kind != OP_GEMV_GROUP || op.M != 1 || op.a_dtype != MVLM_F32 || plan->ops.empty()) return;
+    const Op& a = plan->ops.back();
+    if (a.kind != OP_ATTENTION || a.M != 1 || a.c_dtype != MVLM_F32 || (a.K != 64 && a.K != 128)) return;
+    const size_t q_bytes = (size_t)a.batch * a.K * 2, kv_bytes = (size_t)a.N * a.batch * a.K * 2;
+    const size_t o_bytes = (size_t)a.batch * a.K * 4;
+    bool reads_o = false;
+    for (int i = 0; i < op.gcount; ++i) {
+        const mvlm_weight* w = op.gw[i];
+        const size_t y_bytes = (size_t)w->N * dtype_size(op.gyd[i]);
+        if (overlaps(op.gy[i], y_bytes, a.a, q_bytes) || overlaps(op.gy[i], y_bytes, a.b, kv_bytes) ||
+            overlaps(op.gy[i], y_bytes, a.v, kv_bytes) || overlaps(op.gy[i], y_bytes, a.c, o_bytes))
+            return;
+        if (op.gx[i] == a.c) reads_o = true;
+        else if (overlaps(op.gx[i], (size_t)w->K * 4, a.c, o_bytes)) return;
+        const Epilogue& e = op.gep[i];
+        const size_t eb = (size_t)w->N * dtype_size(e.dtype);
+        if (overlaps(e.bias, eb, a.c, o_bytes) || overlaps(e.mul, eb, a.c, o_bytes) || overlaps(e.res, eb, a.c, o_bytes))
+            return;
+    }
+    if (!reads_o) return;
+    StreamAttnDesc d;
+    d.q = a.a; d.k = a.b; d.v = a.v; d.o = (float*)a.c;
+    d.heads = a.batch; d.head_dim = a.K; d.seq_kv = a.N; d.scale = a.scale;
+    mvlm_device* dev = plan->dev;
+    if (device_scratch(dev, stream_attn_workspace_bytes(d.heads, d.head_dim, d.seq_kv, op.num_cus), &d.workspace) !=
+        MVLM_OK)
+        return;
+    if (hipSetDevice(dev->ordinal) != hipSuccess || hipMalloc(&d.sync, SYNC_BYTES) != hipSuccess) {
+        (void)hipGetLastError();
+        return;
+    }
+    bool ok = hipMemset(d.sync, 0, SYNC_BYTES) == hipSuccess &&
+              stream_attn_check(op.gcount, op.gx, op.a_dtype, op.gw, d, op.num_cus) == hipSuccess;
+    if (ok) {
+        try {
+            plan->sync_areas.push_back(d.sync);
+        } catch (...) {
+            ok = false;
+        }
+    }
+    if (!ok) {
+        (void)hipGetLastError();
+        (void)hipFree(d.sync);
+        return;
+    }
+    op.attn = d;
+    op.attn_fusable = true;
+}
+
+static int plan_push(mvlm_plan* plan, Op op) {
     drop_graph(plan);   // a recorded graph no longer matches
+    mark_fusable(plan, op);
     try {
         plan->ops.push_back(op);
     } catch (...) {
@@ -703,13 +778,55 @@ extern "C" int mvlm_plan_add_argmax(mvlm_plan* plan, const mvlm_buffer* x, int d
     return st != MVLM_OK ? st : plan_push(plan, op);
 }
 
-// The plan's launches in order, one per entry.
+// Whether entry i is launched by entry i + 1 (a decode attention carried by
+// the grouped GEMV after it) and whether entry i carries entry i - 1.
+static bool carried_by_next(const mvlm_plan* plan, size_t i) {
+    return plan->fuse && i + 1 < plan->ops.size() && plan->ops[i + 1].attn_fusable;
+}
+static bool carries_prev(const mvlm_plan* plan, size_t i) { return plan->fuse && plan->ops[i].attn_fusable; }
+
+// The plan's launches in order: one per entry, except attention entries
+// carried by the next entry's launch.
 static int enqueue_all(mvlm_plan* plan) {
-    for (const Op& op : plan->ops) {
-        const hipError_t e = enqueue_op(plan->dev->stream, op);
+    for (size_t i = 0; i < plan->ops.size(); ++i) {
+        if (carried_by_next(plan, i)) continue;
+        const hipError_t e = enqueue_op(plan->dev->stream, plan->ops[i], carries_prev(plan, i));
         if (e != hipSuccess) return check_hip(e, "plan launch");
     }
     return MVLM_OK;
+}
+
+extern "C" int mvlm_plan_set_fusion(mvlm_plan* plan, int enable) {
+    REQUIRE(plan, "mvlm_plan_set_fusion: plan is null");
+    if (plan->fuse != (enable != 0)) drop_graph(plan);
+    plan->fuse = enable != 0;
+    return MVLM_OK;
+}
+
+extern "C" int mvlm_plan_fused(const mvlm_plan* plan) {
+    if (!plan) return MVLM_ERR_INVALID_ARG;
+    int n = 0;
+    for (size_t i = 0; i < plan->ops.size(); ++i) n += carries_prev(plan, i) ? 1 : 0;
+    return n;
+}
+
+extern "C" int mvlm_plan_check(mvlm_plan* plan) {
+    REQUIRE(plan, "mvlm_plan_check: plan is null");
+    mvlm_device* dev = plan->dev;
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    HIP_TRY(hipStreamSynchronize(dev->stream));
+    int failed = 0;
+    for (const Op& op : plan->ops) {
+        if (!op.attn_fusable) continue;
+        uint32_t err = 0;
+        HIP_TRY(hipMemcpy(&err, (const char*)op.attn.sync + SYNC_ERR_OFFSET, 4, hipMemcpyDeviceToHost));
+        if (!err) continue;
+        ++failed;
+        HIP_TRY(hipMemset(op.attn.sync, 0, SYNC_BYTES));   // counters the failed launch left part-way
+    }
+    if (!failed) return MVLM_OK;
+    return set_error(MVLM_ERR_HIP, "mvlm_plan_check: %d fused launch site(s) gave up waiting for their attention "
+                     "after 20 ms; the workgroups that waited stored NaN", failed);
 }
 
 extern "C" int mvlm_plan_use_graph(mvlm_plan* plan, int enable) {
@@ -759,19 +876,24 @@ extern "C" int mvlm_plan_profile(mvlm_plan* plan, float* op_ms, int capacity) {
     hipStream_t s = plan->dev->stream;
     KernelTiming& t = kernel_timing();
     int launched = 0;
+    int last = -1;
     for (int i = 0; i < n && st == MVLM_OK; ++i) {
+        if (carried_by_next(plan, (size_t)i)) continue;   // timed with the launch that carries it
         t.start = ev[2 * i];
         t.stop = ev[2 * i + 1];
-        const hipError_t e = enqueue_op(s, plan->ops[i]);
+        const hipError_t e = enqueue_op(s, plan->ops[i], carries_prev(plan, (size_t)i));
         t = KernelTiming{};
         if (e != hipSuccess) st = check_hip(e, "plan launch");
-        else launched = i + 1;
+        else last = i;
     }
     t = KernelTiming{};
+    launched = last + 1;
     if (st == MVLM_OK && launched > 0)
         st = check_hip(hipEventSynchronize(ev[2 * (size_t)(launched - 1) + 1]), "hipEventSynchronize");
-    for (int i = 0; i < n && st == MVLM_OK; ++i)
-        st = check_hip(hipEventElapsedTime(&op_ms[i], ev[2 * i], ev[2 * i + 1]), "hipEventElapsedTime");
+    for (int i = 0; i < n && st == MVLM_OK; ++i) {
+        if (carried_by_next(plan, (size_t)i)) op_ms[i] = 0.0f;
+        else st = check_hip(hipEventElapsedTime(&op_ms[i], ev[2 * i], ev[2 * i + 1]), "hipEventElapsedTime");
+    }
     for (hipEvent_t e : ev)
         if (e) (void)hipEventDestroy(e);
     return st;

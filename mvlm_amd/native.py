@@ -143,6 +143,9 @@ _SIGNATURES = {
     "mvlm_plan_use_graph": (c_int, [_P, c_int]),
     "mvlm_plan_run": (c_int, [_P, c_int, _PP]),
     "mvlm_plan_profile": (c_int, [_P, POINTER(c_float), c_int]),
+    "mvlm_plan_set_fusion": (c_int, [_P, c_int]),
+    "mvlm_plan_fused": (c_int, [_P]),
+    "mvlm_plan_check": (c_int, [_P]),
     "mvlm_marker_record": (c_int, [_P, _PP]),
     "mvlm_marker_elapsed_ms": (c_int, [_P, _P, POINTER(c_float)]),
     "mvlm_gguf_open": (c_int, [c_char_p, _PP]),
@@ -495,6 +498,24 @@ class Plan:
         ev, want = _ev(event)
         _call("mvlm_plan_run", self.handle, repeats, byref(ev) if want else None)
         return Event(ev) if want else None
+
+    def set_fusion(self, enable=True):
+        """Plan fusion on (default) or off: a decode attention entry runs inside
+        the grouped GEMV launch after it that reads its output."""
+        _call("mvlm_plan_set_fusion", self.handle, 1 if enable else 0)
+        return self
+
+    def fused(self) -> int:
+        """Number of attention entries carried by the launch after them."""
+        n = lib().mvlm_plan_fused(self.handle)
+        if n < 0:
+            raise MvlmError(n, "mvlm_plan_fused", last_error())
+        return n
+
+    def check(self):
+        """Synchronizes; raises MvlmError if a fused launch gave up waiting."""
+        _call("mvlm_plan_check", self.handle)
+        return self
 
     def profile(self) -> np.ndarray:
         n = len(self)

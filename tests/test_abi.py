@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version():
     from mvlm_amd import native
-    assert native.lib().mvlm_abi_version() == 2
+    assert native.lib().mvlm_abi_version() == 3
 
 
 def test_device_count_without_gpu_is_not_an_error():

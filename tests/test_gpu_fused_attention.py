@@ -1,0 +1,218 @@
+"""Plan fusion: a decode attention (one query per head against a KV cache,
+attention_decode in attention.cl:197-295) carried by the grouped GEMV launch
+that reads its output (the output projection after it, moondream2.cpp:423-446).
+
+Checked on the GPU through the C ABI, after every graph replay:
+  * the attention output o against the oracle's fp64 attention, within the
+    tolerance of the attention tests (2^-10 A + seq_kv 2^-24 A + 2 D 2^-24 R A
+    + half an fp32 ulp, A = sum_k p_k |V_k|, R = max_k scale sum_d |q_d k_d|);
+  * the entry reading o as x against the oracle's fp32 GEMV on the o the GPU
+    produced (1e-5 S, S = sum_k |x_k w_k|), the other entry bit-identical to
+    the same plan run unfused, whose o (the matrix-core attention kernel)
+    meets the same bound;
+  * plan.check(): no wait gave up.
+Every replay must give the same bits: the counters the launch hands work
+through return to zero by its end."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import mvlm_amd as m
+
+pytestmark = pytest.mark.gpu
+
+F16, F32 = m.F16, m.F32
+
+
+def f16_bits(x):
+    return np.asarray(x, np.float16).view(np.uint16)
+
+
+def attention_tol(O64, A, R, seq_kv, D):
+    return (2.0 ** -10 + seq_kv * 2.0 ** -24 + 2 * D * 2.0 ** -24 * R[..., None]) * A + np.abs(O64) * 2.0 ** -24 + 1e-12
+
+
+def gemv_check(orc, x, W, y, rows, scratch):
+    deq = W.dequant_rows(rows, scratch).astype(np.float32)
+    K = x.size
+    ref = orc.gemm_nk("f32", np.ascontiguousarray(x.reshape(1, K)), np.ascontiguousarray(deq), 1, len(rows), K)
+    _, S = orc.gemm_f64(x.reshape(1, K).astype(np.float64), deq.astype(np.float64), 1, len(rows), K)
+    err = np.abs(y[rows].astype(np.float64) - ref.reshape(-1))
+    assert np.all(err <= 1e-5 * S.reshape(-1)), float(np.max(err / (1e-5 * S.reshape(-1))))
+
+
+class Case:
+    """attention (q, K, V -> o) then grouped {o -> W1 -> y1, x2 -> W2 -> y2}"""
+
+    def __init__(self, dev, wdt, T, H, D, N1, N2, K2, seed):
+        rng = np.random.default_rng(seed)
+        self.T, self.H, self.D = T, H, D
+        self.q = f16_bits(rng.standard_normal((H, D)))
+        self.k = f16_bits(rng.standard_normal((T, H, D)))
+        self.v = f16_bits(rng.standard_normal((T, H, D)))
+        self.dq, self.dk, self.dv = dev.upload(self.q), dev.upload(self.k), dev.upload(self.v)
+        self.o = dev.alloc(H * D * 4)
+        self.W1 = dev.random_weight(wdt, N1, H * D, seed ^ 0x51, 0.02)
+        self.W2 = dev.random_weight(wdt, N2, K2, seed ^ 0x52, 0.02)
+        self.x2 = dev.fill_normal(dev.alloc(K2 * 4), F32, K2, seed ^ 0x53, 1.0)
+        self.y1, self.y2 = dev.alloc(N1 * 4), dev.alloc(N2 * 4)
+        self.N1, self.N2, self.K2 = N1, N2, K2
+        self.scratch = dev.alloc(max(N1 * H * D, N2 * K2) * 4)
+
+    def plan(self, dev, fuse=True, bias=None):
+        p = m.Plan(dev)
+        p.add_attention(self.dq, self.dk, self.dv, self.o, F32, 1, self.T, self.H, self.D)
+        eps = None if bias is None else [{"bias": bias}, None]
+        p.add_gemv_grouped([(self.o, F32, self.W1, self.y1, F32), (self.x2, F32, self.W2, self.y2, F32)],
+                           epilogues=eps)
+        p.set_fusion(fuse)
+        return p
+
+    def outputs(self):
+        return (self.o.download(np.float32, self.H * self.D), self.y1.download(np.float32, self.N1),
+                self.y2.download(np.float32, self.N2))
+
+    def check_attention(self, orc, o):
+        O64, A, R = orc.attention_f64(self.q[None], self.k, self.v, 1, self.T, self.H, self.D, False,
+                                      1.0 / np.sqrt(self.D))
+        got = o.astype(np.float64).reshape(1, self.H, self.D)
+        tol = attention_tol(O64, A, R, self.T, self.D)
+        err = np.abs(got - O64)
+        assert np.all(np.isfinite(got))
+        assert np.all(err <= tol), float(np.max(err / tol))
+
+    def free(self):
+        self.W1.free()
+        self.W2.free()
+
+
+def run_case(dev, orc, wdt, T, H, D, N1=2048, N2=2048, K2=8192, seed=7, replays=4):
+    print(f"[fused attention] wdt={wdt} T={T} H={H} D={D} N1={N1} N2={N2} K2={K2}", flush=True)
+    c = Case(dev, wdt, T, H, D, N1, N2, K2, seed)
+    ref = c.plan(dev, fuse=False)
+    assert ref.fused() == 0
+    ref.run(1)
+    ref.check()
+    o_ref, y1_ref, y2_ref = c.outputs()
+    fused = c.plan(dev, fuse=True)
+    assert fused.fused() == 1
+    fused.use_graph(True)
+    first = None
+    for r in range(replays):
+        for b in (c.o, c.y1, c.y2):
+            b.zero()
+        fused.run(1)
+        fused.check()
+        o, y1, y2 = c.outputs()
+        if first is None:
+            first = (o, y1, y2)
+            c.check_attention(orc, o)
+            rows = np.unique(np.linspace(0, N1 - 1, 128).astype(np.int64))
+            gemv_check(orc, o, c.W1, y1, rows, c.scratch)
+            assert np.array_equal(y2, y2_ref)
+            c.check_attention(orc, o_ref)
+        else:
+            for a, b in zip(first, (o, y1, y2)):
+                assert np.array_equal(a, b), r
+    fused.destroy()
+    ref.destroy()
+    c.free()
+
+
+@pytest.mark.parametrize("T", [1, 5, 127, 300, 512, 2048, 4100])
+def test_fused_decode_attention_q8_0(dev, orc, T):
+    run_case(dev, orc, m.Q8_0, T, 32, 64)
+
+
+@pytest.mark.parametrize("wdt,T,H,D", [
+    (m.Q4_0, 512, 32, 64),       # Phi-1.5 shapes, Q4_0 weights
+    (m.Q4_0, 2048, 32, 64),
+    (m.F32, 200, 16, 64),        # dense fp32 weights (rows of 4 KiB)
+    (m.F16, 300, 32, 64),
+    (m.Q8_0, 700, 16, 128),      # head_dim 128
+    (m.Q8_0, 9, 3, 64),          # few heads: many splits per head
+    (m.Q4_0, 3000, 5, 128),
+])
+def test_fused_decode_attention_shapes(dev, orc, wdt, T, H, D):
+    run_case(dev, orc, wdt, T, H, D, N1=1000, N2=3000, K2=2048)
+
+
+def test_fused_with_epilogue_and_plan_profile(dev, orc):
+    c = Case(dev, m.Q8_0, 512, 32, 64, 2048, 2048, 8192, 11)
+    bias = dev.fill_normal(dev.alloc(2048 * 4), F32, 2048, 0x77, 0.5)
+    p = c.plan(dev, fuse=True, bias=bias)
+    assert p.fused() == 1
+    p.run(2)
+    p.check()
+    o, y1, _ = c.outputs()
+    c.check_attention(orc, o)
+    rows = np.arange(0, 2048, 16)
+    deq = c.W1.dequant_rows(rows, c.scratch)
+    _, S = orc.gemm_f64(o.reshape(1, -1).astype(np.float64), deq.astype(np.float64), 1, len(rows), 2048)
+    want = deq.astype(np.float64) @ o.astype(np.float64) + bias.download(np.float32, 2048)[rows]
+    assert np.all(np.abs(y1[rows] - want) <= 1.2e-5 * S.reshape(-1) + 1e-6 * np.abs(want))
+    ms = p.profile()
+    assert ms[0] == 0.0 and ms[1] > 0.0       # the attention is timed with the launch carrying it
+    p.check()
+    p.destroy()
+    c.free()
+
+
+def test_fusion_is_refused_where_it_does_not_fit(dev):
+    H, D, T = 32, 64, 64
+    rng = np.random.default_rng(3)
+    q = dev.upload(f16_bits(rng.standard_normal((2, H, D))))
+    k = dev.upload(f16_bits(rng.standard_normal((T, H, D))))
+    v = dev.upload(f16_bits(rng.standard_normal((T, H, D))))
+    o32, o16 = dev.alloc(2 * H * D * 4), dev.alloc(H * D * 2)
+    W = dev.random_weight(m.Q8_0, 512, H * D, 5, 0.02)
+    Wlong = dev.random_weight(m.Q8_0, 512, 4096, 6, 0.02)
+    x = dev.fill_normal(dev.alloc(4096 * 4), F32, 4096, 9, 1.0)
+    y = dev.alloc(512 * 4)
+
+    def pair(o, o_dtype, seq_q, entries, between=False):
+        p = m.Plan(dev)
+        p.add_attention(q, k, v, o, o_dtype, seq_q, T, H, D)
+        if between:
+            p.add_gemv(x, F32, Wlong, y, F32)
+        p.add_gemv_grouped(entries)
+        n = p.fused()
+        p.destroy()
+        return n
+
+    assert pair(o32, F32, 1, [(o32, F32, W, y, F32)]) == 1
+    assert pair(o32, F32, 2, [(o32, F32, W, y, F32)]) == 0          # more than one query
+    assert pair(o32, F32, 1, [(x, F32, W, y, F32)]) == 0            # nothing reads o
+    assert pair(o32, F32, 1, [(o32, F32, W, y, F32)], between=True) == 0
+    assert pair(o32, F32, 1, [(o32, F32, W, q, F32)]) == 0          # an entry writes q
+    assert pair(o32, F32, 1, [(o32, F32, W, o32, F32)]) == 0        # an entry writes o
+    # an F16 output read as the F16 x of dense F16 weights
+    W16 = dev.pack(f16_bits(rng.standard_normal((512, H * D)) * 0.02), F16, 512, H * D)
+    p = m.Plan(dev)
+    p.add_attention(q, k, v, o16, F16, 1, T, H, D)
+    p.add_gemv_grouped([(o16, F16, W16, y, F32)])
+    assert p.fused() == 0
+    p.destroy()
+    W.free()
+    Wlong.free()
+    W16.free()
+
+
+def test_long_rows_reading_o_are_not_fused(dev):
+    H, D, T = 64, 128, 100          # o has 8192 values: Q8_0 rows of 8 KiB of codes
+    rng = np.random.default_rng(4)
+    q = dev.upload(f16_bits(rng.standard_normal((H, D))))
+    k = dev.upload(f16_bits(rng.standard_normal((T, H, D))))
+    v = dev.upload(f16_bits(rng.standard_normal((T, H, D))))
+    o = dev.alloc(H * D * 4)
+    W = dev.random_weight(m.Q8_0, 256, H * D, 8, 0.02)
+    y = dev.alloc(256 * 4)
+    p = m.Plan(dev)
+    p.add_attention(q, k, v, o, F32, 1, T, H, D)
+    p.add_gemv_grouped([(o, F32, W, y, F32)])
+    assert p.fused() == 0
+    p.run(1)
+    p.check()
+    p.destroy()
+    W.free()
