@@ -32,6 +32,7 @@
 #include "gemv_common.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 #include <vector>
 
@@ -771,7 +772,8 @@ static hipError_t launch_group_x(hipStream_t s, int x_dtype, StreamGroup& g, siz
 // workgroup iterations (NWAVE waves x ATTN_NL loads x keys per load).
 static void attn_split(int heads, int D, int seq_kv, int num_cus, int* splits, int* keys_per_split) {
     const int kb = NWAVE * ATTN_NL * (64 / (D / 8));
-    const int want = std::max(1, (num_cus + heads - 1) / heads);
+    int want = std::max(1, (num_cus + heads - 1) / heads);
+    if (const char* e = std::getenv("MVLM_ATTN_SPLITS")) want = std::max(1, std::atoi(e));   // tuning override
     const int s = std::max(1, std::min(std::min((seq_kv + kb - 1) / kb, want), ATTN_MAX_SPLITS));
     const int k = ((seq_kv + s - 1) / s + kb - 1) / kb * kb;
     *keys_per_split = k;
