@@ -178,21 +178,24 @@ def decode_step(dev, m, qt, M, steps, warmup, graph=True, grouped=True):
 
 
 def build_token_plan(dev, m, qt, cache, fuse=True):
-    """The plan of one Phi-1.5 decode step with the path's own ops end to end: per
-    layer the grouped {QKV, fc1} GEMV, attention of the new token against a
-    `cache`-entry fp16 KV cache (32 heads of 64, fp32 output), the grouped
-    {dense, fc2} GEMV with dense reading the attention output; then the LM
-    head and the on-device token pick.  Layer norm, rotary embedding, the KV
-    append and GELU are not part of this path and are left out (q, K and V are
-    fixed stand-ins, the same for every layer).  The grouped launches carry
-    the epilogues of the block's projections: QKV + bias, fc1 + bias + GELU,
-    dense + bias + residual, fc2 + bias + residual (the residual stream h;
-    each branch writes its own output).  fuse: plan fusion, each attention
-    computed inside the {dense, fc2} launch that reads it (74 entries, 50
-    launches); off, every entry is a launch.
+    """The plan of one Phi-1.5 decode step with the path's own ops end to end, in
+    the reference's order (moondream2.cpp:359-541): per layer the grouped
+    {QKV, fc1} GEMV; the decode attention step, which takes q and the new key
+    and value from the QKV output, appends them (fp16) to the layer's KV cache
+    at row `cache` and attends over cache + 1 keys (32 heads of 64, fp32
+    output; kv_cache_append and attention_decode, moondream2.cpp:404-440); the
+    grouped {dense, fc2} GEMV with dense reading the attention output; then the
+    LM head and the on-device token pick.  Layer norm, the rotary embedding and
+    the block's residual sum are not part of this path: every layer reads the
+    same stand-in activations, and its cache holds `cache` random fp16 rows.
+    The grouped launches carry the epilogues of the block's projections:
+    QKV + bias, fc1 + bias + GELU, dense + bias + residual, fc2 + bias +
+    residual (each branch writes its own output).  fuse: plan fusion, each
+    attention step computed inside the {QKV, fc1} launch that writes its
+    q, k and v (74 entries, 50 launches); off, every entry is a launch.
     Returns (plan, weights, io) with io = {"x" (input of each GEMV), "y"
     (PHI_STEP order), "ep" (per GEMV: dict of bias / act / residual buffers,
-    or None), "token", "q", "k", "v", "o"}."""
+    or None), "token", "kc", "vc", "o" (per layer)}."""
     qdt = m.Q8_0 if qt == "q8_0" else m.Q4_0
     weights = [dev.random_weight(qdt, N, K, SEED ^ (0x100 + i), 0.02) for i, (_, N, K) in enumerate(PHI_STEP)]
     x_of = decode_inputs(dev, m, 1)
@@ -204,10 +207,10 @@ def build_token_plan(dev, m, qt, cache, fuse=True):
              "dense": {"bias": bias["dense"], "residual": h}, "fc2": {"bias": bias["fc2"], "residual": h}}
     eps = [ep_of.get(name) for name, _, _ in PHI_STEP]
     H, D = 32, 64
-    q = dev.fill_normal(dev.alloc(H * D * 2), m.F16, H * D, SEED ^ 0x701, 1.0)
-    k = dev.fill_normal(dev.alloc(cache * H * D * 2), m.F16, cache * H * D, SEED ^ 0x702, 1.0)
-    v = dev.fill_normal(dev.alloc(cache * H * D * 2), m.F16, cache * H * D, SEED ^ 0x703, 1.0)
-    o = dev.alloc(H * D * 4)
+    rows = (cache + 1) * H * D
+    kc = [dev.fill_normal(dev.alloc(rows * 2), m.F16, rows, SEED ^ (0x7000 + l), 1.0) for l in range(24)]
+    vc = [dev.fill_normal(dev.alloc(rows * 2), m.F16, rows, SEED ^ (0x7100 + l), 1.0) for l in range(24)]
+    o = [dev.alloc(H * D * 4) for _ in range(24)]
     tok = dev.alloc(4)
     plan = m.Plan(dev)
     plan.set_fusion(fuse)
@@ -216,14 +219,14 @@ def build_token_plan(dev, m, qt, cache, fuse=True):
         plan.add_gemv_grouped([(x_of["qkv"], m.F32, weights[i0], ys[i0], m.F32),
                                (x_of["fc1"], m.F32, weights[i0 + 2], ys[i0 + 2], m.F32)],
                               epilogues=[eps[i0], eps[i0 + 2]])
-        plan.add_attention(q, k, v, o, m.F32, 1, cache, H, D, causal=False)
-        plan.add_gemv_grouped([(o, m.F32, weights[i0 + 1], ys[i0 + 1], m.F32),
+        plan.add_attention_decode_step(ys[i0], kc[layer], vc[layer], o[layer], cache, H, D)
+        plan.add_gemv_grouped([(o[layer], m.F32, weights[i0 + 1], ys[i0 + 1], m.F32),
                                (x_of["fc2"], m.F32, weights[i0 + 3], ys[i0 + 3], m.F32)],
                               epilogues=[eps[i0 + 1], eps[i0 + 3]])
     plan.add_gemv(x_of["lm_head"], m.F32, weights[-1], ys[-1], m.F32, 1)
     plan.add_argmax(ys[-1], m.F32, 1, 51200, 51200, tok)
-    xs = [x_of["qkv"], o, x_of["fc1"], x_of["fc2"]] * 24 + [x_of["lm_head"]]
-    return plan, weights, {"x": xs, "y": ys, "ep": eps, "token": tok, "q": q, "k": k, "v": v, "o": o}
+    xs = [v for layer in range(24) for v in (x_of["qkv"], o[layer], x_of["fc1"], x_of["fc2"])] + [x_of["lm_head"]]
+    return plan, weights, {"x": xs, "y": ys, "ep": eps, "token": tok, "kc": kc, "vc": vc, "o": o}
 
 
 def decode_token(dev, m, qt, cache, steps, warmup, fuse=True):
@@ -237,12 +240,13 @@ def decode_token(dev, m, qt, cache, steps, warmup, fuse=True):
     for W in weights:
         W.free()
     nbytes = (sum(gemv_bytes(qt, N, K, 1) for _, N, K in PHI_STEP)   # weights, x, y
-              + 24 * 2 * cache * 32 * 64 * 2.0                        # the KV cache, fp16
+              + 24 * 2 * (cache + 1) * 32 * 64 * 2.0                  # each layer's KV cache, fp16 (+ the append)
               + 51200 * 4.0)                                          # logits read by the token pick
     return {"workload": f"phi15_decode_token_{qt}_cache{cache}" + ("" if fuse else "_unfused"), "us": ms * 1e3,
             "tokens_per_s": 1e3 / ms, "ops": 24 * 3 + 2, "launches": 24 * 3 + 2 - fused,
-            "attention": ("each layer's attention computed inside its {dense, fc2} launch (plan fusion)" if fused
-                          else "one launch per layer"),
+            "attention": ("each layer's attention step (cache append + attention over cache + 1 keys) computed "
+                          "inside the {QKV, fc1} launch that writes its q, k, v (plan fusion)" if fused
+                          else "one attention step launch per layer (split kernel + merge kernel)"),
             "epilogues": "QKV+bias, fc1+bias+GELU, dense+bias+residual, fc2+bias+residual "
                          "fused into the grouped GEMVs",
             "bytes_per_token": nbytes,

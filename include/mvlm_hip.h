@@ -289,6 +289,20 @@ int mvlm_attention_prefill(mvlm_device* dev, const mvlm_buffer* Q, const mvlm_bu
 int mvlm_attention_decode(mvlm_device* dev, const mvlm_buffer* Q, const mvlm_buffer* K_cache,
                           const mvlm_buffer* V_cache, mvlm_buffer* output, int cache_len,
                           int num_heads, int head_dim, mvlm_event** ev);
+/* One decode step of attention from the fused QKV projection's output, the
+ * sequence of src/models/moondream2.cpp:404-440 without the rotary embedding:
+ * kv_cache_append (moondream2.cpp:305-316, :419) then attention_decode
+ * (attention.cl:197-295) over the grown cache.  qkv: fp32 [3][num_heads]
+ * [head_dim] = q, the new key, the new value.  The new key and value are
+ * rounded to fp16 (RNE) and written to row `cached` of K_cache / V_cache
+ * (fp16 [cached + 1][num_heads][head_dim]); q, rounded to fp16, attends over
+ * the cached + 1 keys with scale (1/sqrt(head_dim) when 0); O: fp32
+ * [num_heads][head_dim].  head_dim 64 or 128, at most 192 heads.  In a plan,
+ * right after the grouped GEMV that writes qkv, it runs inside that GEMV's
+ * launch (see mvlm_plan_set_fusion). */
+int mvlm_attention_decode_step(mvlm_device* dev, const mvlm_buffer* qkv, mvlm_buffer* K_cache,
+                               mvlm_buffer* V_cache, mvlm_buffer* O, int cached, int num_heads,
+                               int head_dim, float scale, mvlm_event** ev);
 
 /* ---- token pick: row-wise argmax on the device ----------------------------
  * Replaces argmax_logits (src/models/moondream2.cpp:553-593), which reads the
@@ -353,6 +367,9 @@ int mvlm_plan_add_gemm_batched(mvlm_plan* plan, const mvlm_buffer* A, const mvlm
 int mvlm_plan_add_attention(mvlm_plan* plan, const mvlm_buffer* Q, const mvlm_buffer* K,
                             const mvlm_buffer* V, mvlm_buffer* O, int o_dtype, int seq_q, int seq_kv,
                             int num_heads, int head_dim, int causal, float scale);
+int mvlm_plan_add_attention_decode_step(mvlm_plan* plan, const mvlm_buffer* qkv, mvlm_buffer* K_cache,
+                                        mvlm_buffer* V_cache, mvlm_buffer* O, int cached, int num_heads,
+                                        int head_dim, float scale);
 int mvlm_plan_add_argmax(mvlm_plan* plan, const mvlm_buffer* x, int dtype, int rows, int n, int64_t ld,
                          mvlm_buffer* out_index);
 /* enable != 0: capture the plan into a HIP graph (now) and replay it on run. */
@@ -365,17 +382,24 @@ int mvlm_plan_run(mvlm_plan* plan, int repeats, mvlm_event** ev);
  * the next entry's launch (plan fusion) reports 0. */
 int mvlm_plan_profile(mvlm_plan* plan, float* op_ms, int capacity);
 /* Plan fusion.  No counterpart in the reference, whose decode loop launches
- * attention_decode and then the output projection
- * (src/models/moondream2.cpp:423-446).  A decode attention entry (seq_q == 1,
- * F32 output, head_dim 64 or 128) followed directly by a grouped M == 1 GEMV
- * entry (F32 x) that reads the attention output as some entries' x runs
- * inside that GEMV's launch: its workgroups come first, and the entries that
- * read the output wait for it after loading their weights.  The pair is
- * fused when the GEMV entry is added and fits (its entries neither write the
- * attention's inputs or output nor read the output except as x, weight rows
- * of at most 4 KiB in HBM (codes only for Q8_0 / Q4_0: K <= 4096 / 8192) for
- * the waiting entries, and those entries' workgroups cannot
- * fill the device alone); otherwise both launch as before.  On by default;
+ * the projections, attention_decode and the output projection one by one
+ * (src/models/moondream2.cpp:369-446).  A decode attention runs inside the
+ * launch of a neighbouring grouped M == 1 GEMV entry:
+ * (1) a decode attention step entry right after the grouped GEMV one of whose
+ *     entries writes its qkv (F32, N = 3 num_heads head_dim): its workgroups
+ *     follow that entry's, load their cached keys and values, and wait for
+ *     the workgroups writing their head's rows; fused when no other entry
+ *     writes qkv, the caches or O and no entry reads the caches or O;
+ * (2) a decode attention entry (seq_q == 1, F32 output, head_dim 64 or 128)
+ *     right before a grouped GEMV (F32 x) some of whose entries read its
+ *     output as x: its workgroups come first, and the entries reading the
+ *     output wait for it after loading their weights; fused when no entry
+ *     writes the attention's inputs or output or reads the output other than
+ *     as x, and the waiting entries have weight rows of at most 4 KiB in HBM
+ *     (codes only for Q8_0 / Q4_0: K <= 4096 / 8192).
+ * Either way the workgroups that wait must not be able to fill the device
+ * alone; otherwise, or with fusion off, both entries launch as before.  The
+ * pair is set up when the second entry is added.  On by default;
  * set_fusion(0) launches every entry separately (drops a captured graph).
  * mvlm_plan_fused returns the number of fused pairs in effect.
  * A waiting workgroup gives up after 20 ms and stores NaN;

@@ -217,28 +217,38 @@ struct StreamAttnDesc;
 hipError_t launch_gemv_stream_group(hipStream_t s, int count, const void* const* xs, int x_dtype,
                                     const mvlm_weight* const* ws, void* const* ys, const int* y_dtypes, int num_cus,
                                     const Epilogue* eps = nullptr, int M = 1, const StreamAttnDesc* at = nullptr);
-// Decode attention (one query per head against seq_kv cached keys; fp16 q
-// [heads][D], K and V [seq_kv][heads][D]; fp32 output o [heads][D]) carried by
-// an M = 1 grouped launch whose problems with x == o read its output: the
-// attention runs in the launch's first workgroups, the problems reading o
-// wait for it after loading their weights (gemv_stream.hip).
+// Decode attention carried by an M = 1 grouped launch (gemv_stream.hip): one
+// query per head against the KV cache (fp16 K and V [.][heads][D], D = 64 or
+// 128), fp32 output o [heads][D].  step == 0: fp16 q [heads][D], `cached`
+// keys.  step != 0: q, the new key and the new value are the three fp32
+// thirds of qkv [3][heads][D]; they are rounded to fp16, the new key and
+// value written to cache row `cached`, and q attends over cached + 1 keys.
+// mode 0: the attention runs in the launch's first workgroups and the
+// problems with x == o wait for it; mode 1 (step only): qkv is the output of
+// one problem of the launch (N = 3 heads D) and the attention runs after that
+// problem's rows are written.
 struct StreamAttnDesc {
     const void* q = nullptr;
-    const void* k = nullptr;
-    const void* v = nullptr;
+    const void* qkv = nullptr;
+    void* k = nullptr;
+    void* v = nullptr;
     float* o = nullptr;
-    int heads = 0, head_dim = 0, seq_kv = 0;
+    int heads = 0, head_dim = 0, cached = 0, mode = 0, step = 0;
     float scale = 0.0f;
-    void* workspace = nullptr;     // stream_attn_workspace_bytes
+    void* workspace = nullptr;     // stream_attn_workspace_bytes(heads, head_dim, keys attended, CUs)
     void* sync = nullptr;          // SYNC_BYTES of the launch site, zeroed before its first launch
 };
-constexpr size_t SYNC_BYTES = 48 * 1024;
+constexpr size_t SYNC_BYTES = 64 * 1024;
 constexpr size_t SYNC_ERR_OFFSET = 256;   // u32 error word of a sync area
 size_t stream_attn_workspace_bytes(int heads, int head_dim, int seq_kv, int num_cus);
-// hipSuccess when this launch can carry the attention: M = 1, fp32 x, head_dim
-// 64 or 128, and the blocks that wait fit on the device at once beside others
+// hipSuccess when this launch can carry the attention: M = 1, head_dim 64 or
+// 128, mode 0 with fp32 x and rows of at most 4 KiB for the waiting problems,
+// mode 1 with one fp32 problem output equal to qkv, and the workgroups that
+// wait unable to fill the device by themselves
 hipError_t stream_attn_check(int count, const void* const* xs, int x_dtype, const mvlm_weight* const* ws,
-                             const StreamAttnDesc& at, int num_cus);
+                             void* const* ys, const int* y_dtypes, const StreamAttnDesc& at, int num_cus);
+// The same attention as launches of its own (no sync area needed).
+hipError_t launch_attn_decode(hipStream_t s, const StreamAttnDesc& d, int num_cus);
 // Skinny GEMM over up to 8 independent problems (quantized weights of one
 // dtype, fp32 X [M][K] and Y [M][N] each, 1 <= M <= 16) in one launch.
 hipError_t launch_gemm_skinny_group(hipStream_t s, int M, int count, const float* const* Xs,

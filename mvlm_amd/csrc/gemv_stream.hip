@@ -59,6 +59,7 @@ struct StreamProblem {
     int block_begin;               // first block of this problem in the grid
     int ep_on;
     int dep;                       // x is the output of the launch's attention (waits for it)
+    int prod;                      // y holds the launch's attention's q, k, v (device-scope stores, flags)
     Epilogue ep;                   // applied to y when ep_on
 };
 
@@ -70,60 +71,86 @@ constexpr int NWAVE = MVLM_STREAM_WAVES;   // waves per block
 
 // ---- decode attention carried by a grouped launch ----------------------------
 //
-// Phi-1.5's decode attention (one query per head against the KV cache, the
-// work of attention_decode, src/kernels/attention.cl:197-295) sits between its
-// grouped {QKV, fc1} and {dense, fc2} GEMVs.  As a launch of its own it costs
-// a kernel boundary for ~4 MB of cache reads.  Here it runs in the first
-// workgroups of the {dense, fc2} launch instead:
-//  * attention workgroup (head h, key split s) streams its keys and values
-//    (online softmax per wave, merged across waves in LDS) and leaves a
-//    partial result: unnormalised output, running max, sum of weights; the
-//    last split of a head to finish (a device-scope counter per head) merges
-//    the splits, writes o[h] and bumps the launch's done counter;
-//  * workgroups of the problems whose x is o issue their weight loads first,
-//    then wait (one lane polls) until every head is done, then stage o in
-//    LDS.
-// The counters live in a sync area of the launch site (one per fused plan
-// entry, zeroed once) and only ever grow, so no launch resets anything and
-// no atomic is awaited by every waiting workgroup (a counter that 256
+// Decode attention: one new query per head against the KV cache (the work of
+// attention_decode, src/kernels/attention.cl:197-295).  Phi-1.5 runs it
+// between its grouped {QKV, fc1} and {dense, fc2} GEMVs; as a launch of its
+// own it costs a kernel boundary for ~4 MB of cache reads.  A grouped launch
+// can carry it instead, in one of two ways:
+//  * before its readers (mode 0, mvlm_plan_add_attention): the attention's
+//    workgroups come first in the {dense, fc2} launch; the workgroups of the
+//    problems whose x is o issue their weight loads, wait (one lane polls)
+//    until every head is done, then stage o in LDS;
+//  * after its producer (mode 1, mvlm_plan_add_attention_decode_step): q and
+//    the new key and value are the three thirds of one problem's output (the
+//    fused QKV projection, moondream2.cpp:369-440 with the cache append of
+//    :305-316, :419); the attention's workgroups follow that problem's in the
+//    {QKV, fc1} launch, load their cached keys and values, wait for the
+//    producer workgroups that write their head's rows, then append the new
+//    key and value to the cache (fp16) and attend over cached + 1 keys.  The
+//    next launch reads o after a kernel boundary.
+// Attention workgroup (head h, key split s) runs an online softmax per wave,
+// merges its waves in LDS and stores a partial result (unnormalised output,
+// running max, sum of weights); the last split of a head to finish (a
+// device-scope counter per head) merges the splits and writes o[h].
+// Counters live in a sync area of the launch site (one per fused plan entry,
+// zeroed once) and only ever grow, so no launch resets anything and no
+// atomic is awaited by every waiting workgroup (a counter that 256
 // workgroups bump serialises for ~3 us):
-//   byte 0      u64  done: heads finished over all launches; the bump that
-//                    completes a launch's heads writes go = launches so far
+//   byte 0      u64  done (mode 0): heads finished over all launches; the
+//                    bump that completes a launch's heads writes go
 //   byte 256    u32  error word
-//   byte 1024   u32  go[16], 128 bytes apart (the waiting workgroups poll
-//                    go[c % 16], spreading the polls over 16 lines)
-//   byte 4096   u64  head[h], 64 bytes apart: splits of head h finished;
-//                    the bump reaching a multiple of splits merges
-//   byte 16384  u32  seen[c]: launches waiting workgroup c has waited
+//   byte 1024   u32  go[16] (mode 0), 128 bytes apart: launches completed;
+//                    waiting workgroup c polls go[c % 16]
+//   byte 4096   u64  head[h], 64 bytes apart: splits of head h finished; the
+//                    bump reaching a multiple of splits merges
+//   byte 16384  u32  seen[c] (mode 0): launches waiting workgroup c has waited
 //                    through (its own word: it waits for go >= seen + 1)
+//   byte 32768  u32  flag[j] (mode 1): launches producer workgroup j has
+//                    finished (raised once its output stores are complete)
+//   byte 49152  u32  aseen[b] (mode 1): launches attention workgroup b has
+//                    waited through
 // Launches of one site run one after another on the stream, so each
 // launch's counts are whole multiples when the next begins.
-// Only the waiting workgroups wait, and only on workgroups that never wait,
-// so the launch completes as long as the waiting ones cannot fill the device
-// by themselves (checked on the host against the kernel's occupancy).  A
-// wait still gives up after 20 ms: the workgroup then stores NaN instead of
-// its outputs and sets the error word (read by mvlm_plan_check, which then
-// clears the area).
-// Data crossing workgroups (partials, o) moves with device-scope (sc1) stores
-// and loads, and every such store is complete (s_waitcnt vmcnt(0)) before
-// the counter that publishes it is bumped.
-constexpr int SYNC_DONE_B = 0, SYNC_ERR_B = (int)SYNC_ERR_OFFSET, SYNC_GO_B = 1024, SYNC_HEAD_B = 4096, SYNC_SEEN_B = 16384;
+// Only workgroups that wait (mode 0: the readers of o; mode 1: the attention)
+// wait, and only on workgroups that never wait, so the launch completes as
+// long as the waiting ones cannot fill the device by themselves (checked on
+// the host against the kernel's occupancy).  A wait still gives up after
+// 20 ms: the workgroup then stores NaN instead of its outputs and sets the
+// error word (read by mvlm_plan_check, which then clears the area).
+// Data crossing workgroups (producer rows, partials, o) moves with
+// device-scope (sc1) stores and loads, and every such store is complete
+// (s_waitcnt vmcnt(0)) before the counter or flag that publishes it.
+constexpr int SYNC_DONE_B = 0, SYNC_ERR_B = (int)SYNC_ERR_OFFSET, SYNC_GO_B = 1024, SYNC_HEAD_B = 4096,
+              SYNC_SEEN_B = 16384, SYNC_FLAG_B = 32768, SYNC_ASEEN_B = 49152;
 constexpr int SYNC_GO_N = 16;
 constexpr int ATTN_MAX_HEADS = (SYNC_SEEN_B - SYNC_HEAD_B) / 64;
-constexpr int ATTN_MAX_CONSUMERS = (int)(SYNC_BYTES - SYNC_SEEN_B) / 4;
+constexpr int ATTN_MAX_CONSUMERS = (SYNC_FLAG_B - SYNC_SEEN_B) / 4;
+constexpr int ATTN_MAX_PRODUCERS = (SYNC_ASEEN_B - SYNC_FLAG_B) / 4;
+constexpr int ATTN_MAX_BLOCKS = ((int)SYNC_BYTES - SYNC_ASEEN_B) / 4;
+static_assert(SYNC_BYTES == 65536, "sync area layout");
 constexpr int ATTN_NL = 2;                     // key (and value) loads per lane and iteration
 constexpr int ATTN_MAX_SPLITS = 32;
 constexpr uint64_t ATTN_TIMEOUT = 2000000;     // s_memrealtime ticks (100 MHz): 20 ms
 
 struct StreamAttn {
-    const uint16_t* q;         // [heads][D]
-    const uint16_t* k;         // [seq_kv][heads][D]
-    const uint16_t* v;
+    const uint16_t* q;         // mode 0: fp16 [heads][D]
+    const float* qkv;          // mode 1: fp32 [3][heads][D]: q, new key, new value
+    uint16_t* k;               // fp16 caches [.][heads][D]: rows [0, cached) read; mode 1 writes row `cached`
+    uint16_t* v;
     float* o;                  // [heads][D]
     float* part_o;             // [heads][splits][D] unnormalised outputs of the splits
     float* part_ml;            // [heads][splits][2] running max (exp2 domain) and sum of weights
-    uint8_t* sync;             // the site's sync area
-    int heads, D, seq_kv, splits, keys_per_split, blocks, consumers;
+    uint8_t* sync;             // the site's sync area (merge != 0)
+    int heads, D;
+    int cached;                // keys read from the cache
+    int seq_kv;                // keys attended: cached (mode 0), cached + 1 (mode 1)
+    int splits, keys_per_split, blocks;
+    int first;                 // grid index of the first attention workgroup
+    int mode;                  // 0: before the problems reading o; 1: after the problem writing qkv
+    int step;                  // q, the new key and value from qkv, appended to the caches
+    int merge;                 // the last split merges (else attn_merge_kernel does)
+    int consumers;             // mode 0: workgroups that wait for o
+    int prod_rpb, prod_blocks; // mode 1: the producer problem's rows per workgroup and workgroups (first in the grid)
     float scale_log2;          // scale * log2(e)
 };
 
@@ -156,10 +183,17 @@ __device__ __forceinline__ uint64_t first_lane64(uint64_t v) {
     const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
     return ((uint64_t)hi << 32) | lo;
 }
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+__device__ __forceinline__ float f16_round(float x) { return f16_bits_to_f32(f32_to_f16_bits(x)); }
 
 // Head h's o is stored and complete: count it; the count completing a
-// launch's heads publishes the launch number in every go line.
+// launch's heads publishes the launch number in every go line (mode 0).
 __device__ __forceinline__ void attn_head_done(const StreamAttn& a, int lane) {
+    if (a.mode != 0) return;
     uint64_t old = 0;
     if (lane == 0) old = sync_add64(sync_word<uint64_t>(a, SYNC_DONE_B));
     const uint64_t n = first_lane64(old) + 1;
@@ -167,22 +201,101 @@ __device__ __forceinline__ void attn_head_done(const StreamAttn& a, int lane) {
         sync_store(sync_word<uint32_t>(a, SYNC_GO_B + 128 * lane), (uint32_t)(n / (uint64_t)a.heads));
 }
 
-// One attention workgroup: keys [k0, k1) of head h.  Wave w takes keys
+// Mode 1, attention workgroup b of head h: wait until every producer
+// workgroup writing rows [h D, h D + D) of each third of qkv has raised its
+// flag to aseen[b] + 1, and count the launch in aseen[b].  False when the
+// wait gave up.
+__device__ __forceinline__ bool attn_wait_producers(const StreamAttn& a, int b, int h, int wave, int lane,
+                                                    uint32_t* flag_ok) {
+    if (wave == 0) {
+        uint32_t* aseen = sync_word<uint32_t>(a, SYNC_ASEEN_B + 4 * b);
+        const uint32_t want = __builtin_amdgcn_readfirstlane(sync_load(aseen)) + 1;
+        const uint32_t* flags = sync_word<uint32_t>(a, SYNC_FLAG_B);
+        const int per = (a.D - 1) / a.prod_rpb + 2;   // workgroups a range of D rows can touch
+        bool ok = true;
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        while (true) {
+            bool up = true;
+            for (int i = lane; i < 3 * per; i += 64) {
+                const int third = i / per, t = i - third * per;
+                const int r0 = third * a.heads * a.D + h * a.D;
+                const int j = r0 / a.prod_rpb + t;
+                if (j <= (r0 + a.D - 1) / a.prod_rpb) up &= (int32_t)(sync_load(flags + j) - want) >= 0;
+            }
+            if (__builtin_amdgcn_ballot_w64(!up) == 0) break;
+            if (__builtin_amdgcn_s_memrealtime() - t0 > ATTN_TIMEOUT) {
+                ok = false;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        if (lane == 0) {
+            sync_store(aseen, want);
+            if (!ok) sync_store(sync_word<uint32_t>(a, SYNC_ERR_B), 1u);
+            *flag_ok = ok ? 1u : 0u;
+        }
+    }
+    lds_barrier();
+    return *flag_ok != 0;
+}
+
+// A producer workgroup (mode 1) has stored its rows with device-scope stores:
+// once every wave's stores are complete, raise its flag.
+__device__ __forceinline__ void attn_producer_done(const StreamAttn& a, int j, int wave, int lane) {
+    stores_complete();
+    lds_barrier();
+    if (wave == 0 && lane == 0) {
+        uint32_t* flag = sync_word<uint32_t>(a, SYNC_FLAG_B + 4 * j);
+        sync_store(flag, sync_load(flag) + 1);   // its own word: no other writer
+    }
+}
+
+// One attention workgroup b: keys [k0, k1) of head h.  Wave w takes keys
 // k0 + 16w + 128i .. (D = 64; 8 lanes of 16 bytes per key, ATTN_NL keys per
-// lane and iteration), scores in the exp2 domain.
+// lane and iteration), scores in the exp2 domain.  In mode 1 the split that
+// holds key `cached` takes the new key from qkv (wave 0) and writes it and
+// the new value to the caches.  flag_ok: one word of LDS for the wait.
 template <int D>
-__device__ void attn_decode_block(const StreamAttn& a, float* lds, int wave, int lane) {
+__device__ void attn_decode_block(const StreamAttn& a, int b, float* lds, uint32_t* flag_ok, int wave, int lane) {
     constexpr int LPK = D / 8;                 // lanes per key
     constexpr int KPI = 64 / LPK;              // keys per wave-wide load
     constexpr int KPW = ATTN_NL * KPI;         // keys per wave and iteration
     constexpr int DPL = D / 64;                // output dims per lane in the merges
-    const int h = (int)blockIdx.x / a.splits, sp = (int)blockIdx.x - h * a.splits;
+    const int h = b / a.splits, sp = b - h * a.splits;
     const int k0 = sp * a.keys_per_split, k1 = min(k0 + a.keys_per_split, a.seq_kv);
+    const int kc1 = min(k1, a.cached);         // this split's keys in the cache: [k0, kc1)
     const int sub = lane % LPK, kl = lane / LPK;
     const int64_t key_stride = (int64_t)a.heads * D;
     const int col = h * D + sub * 8;
+    // the first iteration's keys and values (they do not depend on the producers)
+    u32x4 kr[ATTN_NL], vr[ATTN_NL];
+    int base = k0 + wave * KPW;
+    auto load_kv = [&](int at) {
+#pragma unroll
+        for (int j = 0; j < ATTN_NL; ++j) {
+            const int64_t r = min(at + j * KPI + kl, kc1 - 1);
+            kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.k + r * key_stride + col));
+        }
+#pragma unroll
+        for (int j = 0; j < ATTN_NL; ++j) {
+            const int64_t r = min(at + j * KPI + kl, kc1 - 1);
+            vr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.v + r * key_stride + col));
+        }
+    };
+    if (base < kc1) load_kv(base);
+    bool ok = true;
     float qf[8];
-    {
+    if (a.step) {
+        if (a.mode == 1 && a.prod_blocks > 0) ok = attn_wait_producers(a, b, h, wave, lane, flag_ok);
+        const __amdgpu_buffer_rsrc_t qr = dev_rsrc(a.qkv, 3 * a.heads * D * 4);
+        const u32x4 u0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, col * 4, 0, kCpolDevice));
+        const u32x4 u1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, col * 4 + 16, 0, kCpolDevice));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            qf[e] = f16_round(__uint_as_float(u0[e])) * a.scale_log2;
+            qf[4 + e] = f16_round(__uint_as_float(u1[e])) * a.scale_log2;
+        }
+    } else {
         const u32x4 u = *reinterpret_cast<const u32x4*>(a.q + col);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -193,52 +306,74 @@ __device__ void attn_decode_block(const StreamAttn& a, float* lds, int wave, int
     float m = -INFINITY, l = 0.0f, o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = 0.0f;
-    for (int base = k0 + wave * KPW; base < k1; base += NWAVE * KPW) {
-        u32x4 kr[ATTN_NL], vr[ATTN_NL];
-        int key[ATTN_NL];
+    // online softmax over N keys of the wave (one per lane group): packed fp16
+    // key and value rows of this lane's 8 dims; keys with valid false score -inf
+    auto process = [&](const u32x4* kp, const u32x4* vp, const bool* valid, auto n_keys) {
+        constexpr int N = decltype(n_keys)::value;
+        float s[N], mx = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < ATTN_NL; ++j) {
-            key[j] = base + j * KPI + kl;
-            const int64_t r = min(key[j], k1 - 1);
-            kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.k + r * key_stride + col));
-        }
-#pragma unroll
-        for (int j = 0; j < ATTN_NL; ++j) {
-            const int64_t r = min(key[j], k1 - 1);
-            vr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.v + r * key_stride + col));
-        }
-        float s[ATTN_NL], mx = -INFINITY;
-#pragma unroll
-        for (int j = 0; j < ATTN_NL; ++j) {
+        for (int j = 0; j < N; ++j) {
             float d = 0.0f;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                d = __builtin_fmaf(qf[2 * e], f16_bits_to_f32((uint16_t)(kr[j][e] & 0xFFFFu)), d);
-                d = __builtin_fmaf(qf[2 * e + 1], f16_bits_to_f32((uint16_t)(kr[j][e] >> 16)), d);
+                d = __builtin_fmaf(qf[2 * e], f16_bits_to_f32((uint16_t)(kp[j][e] & 0xFFFFu)), d);
+                d = __builtin_fmaf(qf[2 * e + 1], f16_bits_to_f32((uint16_t)(kp[j][e] >> 16)), d);
             }
 #pragma unroll
             for (int off = 1; off < LPK; off <<= 1) d += __shfl_xor(d, off);
-            s[j] = key[j] < k1 ? d : -INFINITY;
+            s[j] = valid[j] ? d : -INFINITY;
             mx = fmaxf(mx, s[j]);
         }
 #pragma unroll
         for (int off = LPK; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-        const float mn = fmaxf(m, mx);               // finite: key `base` is below k1
+        const float mn = fmaxf(m, mx);               // finite: the first key of the group is real
         const float alpha = __builtin_amdgcn_exp2f(m - mn);
         l *= alpha;
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] *= alpha;
 #pragma unroll
-        for (int j = 0; j < ATTN_NL; ++j) {
+        for (int j = 0; j < N; ++j) {
             const float p = __builtin_amdgcn_exp2f(s[j] - mn);
             l += p;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                o[2 * e] = __builtin_fmaf(p, f16_bits_to_f32((uint16_t)(vr[j][e] & 0xFFFFu)), o[2 * e]);
-                o[2 * e + 1] = __builtin_fmaf(p, f16_bits_to_f32((uint16_t)(vr[j][e] >> 16)), o[2 * e + 1]);
+                o[2 * e] = __builtin_fmaf(p, f16_bits_to_f32((uint16_t)(vp[j][e] & 0xFFFFu)), o[2 * e]);
+                o[2 * e + 1] = __builtin_fmaf(p, f16_bits_to_f32((uint16_t)(vp[j][e] >> 16)), o[2 * e + 1]);
             }
         }
         m = mn;
+    };
+    for (; base < kc1; base += NWAVE * KPW) {
+        bool valid[ATTN_NL];
+#pragma unroll
+        for (int j = 0; j < ATTN_NL; ++j) valid[j] = base + j * KPI + kl < kc1;
+        process(kr, vr, valid, std::integral_constant<int, ATTN_NL>{});
+        if (base + NWAVE * KPW < kc1) load_kv(base + NWAVE * KPW);
+    }
+    if (a.step && k1 == a.seq_kv && wave == 0) {   // the new key, index `cached`
+        const __amdgpu_buffer_rsrc_t qr = dev_rsrc(a.qkv, 3 * a.heads * D * 4);
+        u32x4 kb[1], vb[1];
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int off = col * 4 + 16 * half;
+            const u32x4 kf = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                           qr, a.heads * D * 4 + off, 0, kCpolDevice));
+            const u32x4 vf = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                           qr, 2 * a.heads * D * 4 + off, 0, kCpolDevice));
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                kb[0][2 * half + e] = (uint32_t)f32_to_f16_bits(__uint_as_float(kf[2 * e])) |
+                                      ((uint32_t)f32_to_f16_bits(__uint_as_float(kf[2 * e + 1])) << 16);
+                vb[0][2 * half + e] = (uint32_t)f32_to_f16_bits(__uint_as_float(vf[2 * e])) |
+                                      ((uint32_t)f32_to_f16_bits(__uint_as_float(vf[2 * e + 1])) << 16);
+            }
+        }
+        const bool valid[1] = {kl == 0};
+        process(kb, vb, valid, std::integral_constant<int, 1>{});
+        if (kl == 0) {   // the cache append: row `cached` of head h, this lane's 8 dims
+            *reinterpret_cast<u32x4*>(a.k + (int64_t)a.cached * key_stride + col) = kb[0];
+            *reinterpret_cast<u32x4*>(a.v + (int64_t)a.cached * key_stride + col) = vb[0];
+        }
     }
     // sums over the wave's key groups: lanes of one sub end with the wave's totals
 #pragma unroll
@@ -273,6 +408,11 @@ __device__ void attn_decode_block(const StreamAttn& a, float* lds, int wave, int
 #pragma unroll
         for (int t = 0; t < DPL; ++t) acc[t] = __builtin_fmaf(lds[w * (D + 2) + lane + 64 * t], f, acc[t]);
     }
+    if (!ok) {   // a wait gave up: NaN out
+        M = __builtin_nanf("");
+#pragma unroll
+        for (int t = 0; t < DPL; ++t) acc[t] = M;
+    }
     const __amdgpu_buffer_rsrc_t orr = dev_rsrc(a.o + h * D, D * 4);
     if (a.splits == 1) {
 #pragma unroll
@@ -293,6 +433,7 @@ __device__ void attn_decode_block(const StreamAttn& a, float* lds, int wave, int
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, M), pmr, sp * 8, 0, kCpolDevice);
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, L), pmr, sp * 8 + 4, 0, kCpolDevice);
     }
+    if (!a.merge) return;   // attn_merge_kernel combines the splits
     stores_complete();
     uint64_t arrived = 0;
     if (lane == 0) arrived = sync_add64(sync_word<uint64_t>(a, SYNC_HEAD_B + 64 * h));
@@ -349,9 +490,10 @@ __device__ void attn_decode_block(const StreamAttn& a, float* lds, int wave, int
     attn_head_done(a, lane);
 }
 
-// Waiting workgroup c (of the launch's consumers): wait until this launch's
-// heads are all done, i.e. go >= seen[c] + 1, and count the launch in
-// seen[c] (lane 0 of wave 0).  Returns false when the wait gave up (the
+
+// Mode 0, waiting workgroup c (of the launch's consumers): wait until this
+// launch's heads are all done, i.e. go >= seen[c] + 1, and count the launch
+// in seen[c] (lane 0 of wave 0).  Returns false when the wait gave up (the
 // workgroup then stores NaN).
 __device__ __forceinline__ bool attn_wait(const StreamAttn& a, int wave, int lane, uint32_t* flag) {
     if (wave == 0 && lane == 0) {
@@ -372,10 +514,39 @@ __device__ __forceinline__ bool attn_wait(const StreamAttn& a, int wave, int lan
         if (!ok) sync_store(sync_word<uint32_t>(a, SYNC_ERR_B), 1u);
         *flag = ok;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    lds_barrier();
     return *flag != 0;
+}
+
+// A decode attention on its own: its workgroups only (no wait), partials to
+// the workspace, then attn_merge_kernel.
+template <int D>
+__global__ __launch_bounds__(64 * NWAVE) void attn_split_kernel(const StreamAttn a) {
+    __shared__ float lds[NWAVE * (D + 2)];
+    __shared__ uint32_t flag_ok;
+    attn_decode_block<D>(a, (int)blockIdx.x, lds, &flag_ok, __builtin_amdgcn_readfirstlane(threadIdx.x >> 6),
+                         threadIdx.x & 63);
+}
+
+// o[h] from head h's split partials: one wave per head, lane d owns dims d + 64 t.
+template <int D>
+__global__ __launch_bounds__(64) void attn_merge_kernel(const StreamAttn a) {
+    const int h = blockIdx.x, lane = threadIdx.x, S = a.splits;
+    const float* ml = a.part_ml + (int64_t)h * S * 2;
+    const float* po = a.part_o + (int64_t)h * S * D;
+    float M = -INFINITY;
+    for (int s = 0; s < S; ++s) M = fmaxf(M, ml[2 * s]);
+    float L = 0.0f, acc[D / 64];
+#pragma unroll
+    for (int t = 0; t < D / 64; ++t) acc[t] = 0.0f;
+    for (int s = 0; s < S; ++s) {
+        const float f = __builtin_amdgcn_exp2f(ml[2 * s] - M);
+        L = __builtin_fmaf(ml[2 * s + 1], f, L);
+#pragma unroll
+        for (int t = 0; t < D / 64; ++t) acc[t] = __builtin_fmaf(po[s * D + lane + 64 * t], f, acc[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < D / 64; ++t) a.o[h * D + lane + 64 * t] = acc[t] / L;
 }
 
 // Work shape of one wave by row length in 1 KiB chunks: R rows x CW chunks,
@@ -389,9 +560,9 @@ struct Shape { int max_chunks, R, CW, SPLIT; };
 constexpr Shape kShapes[] = {{1, 4, 1, 1}, {2, 2, 2, 1}, {4, 1, 4, 1}, {8, 1, 4, 2}, {16, 1, 8, 2}, {8, 2, 4, 2},
                              {2, 1, 2, 1}};
 constexpr int kNumShapes = 7, kByLength = 5, kBatchLong = 5, kFewRows2 = 6;
-// Shapes a problem that waits for the launch's attention may take: rows of at
-// most 4 KiB in HBM (with longer rows the registers holding the code loads
-// during the wait push the kernel past its register budget).
+// Shapes a problem that waits for the launch's attention (or writes its q, k
+// and v) may take: rows of at most 4 KiB in HBM (with longer rows the
+// registers holding the code loads push the kernel past its register budget).
 constexpr bool kDepShape[] = {true, true, true, false, false, false, true};
 static_assert(sizeof(kShapes) / sizeof(kShapes[0]) == kNumShapes, "one kernel case per shape");
 
@@ -400,12 +571,14 @@ static_assert(sizeof(kShapes) / sizeof(kShapes[0]) == kNumShapes, "one kernel ca
 // LDS byte m * x_stride; rows of x at or past M repeat row M-1 and are not
 // stored).  x and the scales are already being staged into LDS (staging loads
 // were issued before these and complete first).
-// With DEP, x is the launch's attention output and not staged yet: the wave
-// waits for the attention after issuing its code loads, then stages x.
-template <class F, typename XT, int MX, int R, int CW, int SPLIT, bool DEP>
+// ROLE 1 (a problem reading the launch's attention output): x is not staged
+// yet; the wave waits for the attention after issuing its code loads, then
+// stages x.  y_device: y (fp32) goes out with device-scope stores (the
+// producer of the launch's attention's q, k, v).
+template <class F, typename XT, int MX, int R, int CW, int SPLIT, int ROLE>
 __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int rb1, int64_t s_base, int x_stride,
                                             int x_region, uint8_t* lds, float (*part)[4 * MX], int wave,
-                                            int lane, const StreamAttn& at, uint32_t* wait_ok) {
+                                            int lane, const StreamAttn& at, uint32_t* wait_ok, bool y_device) {
     constexpr int WPL = F::WPL;
     constexpr int XB = WPL * (int)sizeof(XT);        // x bytes per lane per chunk
     constexpr int SL = XB >= 16 ? XB / 16 : 1;       // 16-byte LDS slots per lane per chunk
@@ -454,7 +627,7 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
 
     // staging done for every wave -> x and scales from LDS, chunk by chunk
     bool ok = true;
-    if constexpr (DEP) {
+    if constexpr (ROLE == 1) {
         ok = attn_wait(at, wave, lane, wait_ok);
         stage_to_lds<(XB >= 16 ? 16 : 4), SL, NWAVE, kCpolDevice>(lds, (const uint8_t*)P.x, K * (int)sizeof(XT),
                                                                     wave, lane);
@@ -564,8 +737,11 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
     // y[m][row] (and the epilogue's mul / residual [m][row], bias [row]),
     // the NV outputs of a wave stored by NV lanes at once
     auto store_row = [&](int row, int m, float v) {
-        if constexpr (DEP) v = ok ? v : __builtin_nanf("");
-        if constexpr (MX == 1) {
+        if constexpr (ROLE == 1) v = ok ? v : __builtin_nanf("");
+        if (MX == 1 && y_device) {   // fp32 y (checked on the host), read by other workgroups of the launch
+            const float out = P.ep_on ? apply_epilogue(P.ep, v, row, row) : v;
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(out), dev_rsrc(P.y, P.N * 4), row * 4, 0, kCpolDevice);
+        } else if constexpr (MX == 1) {
             store_out(P.y, row, P.ep_on ? apply_epilogue(P.ep, v, row, row) : v, P.y_dtype);
         } else {
             const int64_t idx = (int64_t)m * P.N + row;
@@ -594,8 +770,9 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
 // registers.  Issue order: x and scale staging, then every code load, then
 // the wait for the staging alone (vmcnt counts in issue order), the block
 // barrier, the LDS reads, and the wait for the codes.
-// ATTN: the launch's first at.blocks workgroups compute the decode attention
-// (attn_decode_block); the problems marked dep read its output as x.
+// ATTN: workgroups [at.first, at.first + at.blocks) compute the decode
+// attention (attn_decode_block); the problems marked dep read its output as
+// x, the problem marked prod writes its q, k and v.
 template <class F, typename XT, int MX, bool ATTN>
 __global__ __launch_bounds__(64 * NWAVE, MX == 1 ? F::MIN_WAVES : F::MIN_WAVES_BATCH) void gemv_stream_kernel(
     const StreamGroup g) {
@@ -609,9 +786,10 @@ __global__ __launch_bounds__(64 * NWAVE, MX == 1 ? F::MIN_WAVES : F::MIN_WAVES_B
     // loops and row offsets are scalar code
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if constexpr (ATTN) {
-        if ((int)blockIdx.x < g.at.blocks) {
-            if (g.at.D == 64) attn_decode_block<64>(g.at, reinterpret_cast<float*>(lds), wave, lane);
-            else attn_decode_block<128>(g.at, reinterpret_cast<float*>(lds), wave, lane);
+        const int b = (int)blockIdx.x - g.at.first;
+        if (b >= 0 && b < g.at.blocks) {
+            if (g.at.D == 64) attn_decode_block<64>(g.at, b, reinterpret_cast<float*>(lds), &wait_ok, wave, lane);
+            else attn_decode_block<128>(g.at, b, reinterpret_cast<float*>(lds), &wait_ok, wave, lane);
             return;
         }
     }
@@ -651,11 +829,11 @@ __global__ __launch_bounds__(64 * NWAVE, MX == 1 ? F::MIN_WAVES : F::MIN_WAVES_B
         constexpr int si = decltype(shape)::value;
         constexpr Shape S = kShapes[si];
         if (ATTN && kDepShape[si] && dep)
-            stream_rows<F, XT, MX, S.R, S.CW, S.SPLIT, ATTN>(P, rb0, rb1, s_base, x_stride, x_region, lds, part, wave,
-                                                             lane, g.at, &wait_ok);
+            stream_rows<F, XT, MX, S.R, S.CW, S.SPLIT, ATTN ? 1 : 0>(P, rb0, rb1, s_base, x_stride, x_region, lds, part,
+                                                                     wave, lane, g.at, &wait_ok, false);
         else
-            stream_rows<F, XT, MX, S.R, S.CW, S.SPLIT, false>(P, rb0, rb1, s_base, x_stride, x_region, lds, part, wave,
-                                                              lane, g.at, &wait_ok);
+            stream_rows<F, XT, MX, S.R, S.CW, S.SPLIT, 0>(P, rb0, rb1, s_base, x_stride, x_region, lds, part, wave,
+                                                          lane, g.at, &wait_ok, ATTN && P.prod);
     };
     switch (P.shape) {
         case 0: rows(std::integral_constant<int, 0>{}); break;
@@ -670,6 +848,8 @@ __global__ __launch_bounds__(64 * NWAVE, MX == 1 ? F::MIN_WAVES : F::MIN_WAVES_B
             if constexpr (MX > 1) rows(std::integral_constant<int, kBatchLong>{});
             break;
     }
+    if constexpr (ATTN)
+        if (P.prod) attn_producer_done(g.at, (int)blockIdx.x - P.block_begin, wave, lane);
 }
 
 // ---- launch configuration ----------------------------------------------------
@@ -731,10 +911,18 @@ int stream_max_group() { return MAX_GROUP; }
 // x, so x traffic grows with the block count, and part-filled blocks idle
 // waves.  Computing block bounds by division, even once per block, also cost
 // ~0.2 us per launch.)
-// The attention's workgroups come first; the problems' blocks follow.
+// Block order: mode 0, the attention's workgroups, then the problems' (those
+// that wait for it last); mode 1, the producer problem's, the attention's,
+// then the other problems'.
 static unsigned partition(StreamGroup& g) {
-    unsigned begin = (unsigned)g.at.blocks;
+    unsigned begin = 0;
     g.at.consumers = 0;
+    bool placed = g.at.blocks == 0;
+    if (!placed && g.at.mode == 0) {
+        g.at.first = 0;
+        begin = (unsigned)g.at.blocks;
+        placed = true;
+    }
     for (int i = 0; i < g.count; ++i) {
         StreamProblem& p = g.p[i];
         p.rows_per_block = rows_per_block(p.shape);
@@ -742,6 +930,15 @@ static unsigned partition(StreamGroup& g) {
         const unsigned nblk = (unsigned)((p.N + p.rows_per_block - 1) / p.rows_per_block);
         begin += nblk;
         if (p.dep) g.at.consumers += (int)nblk;
+        if (p.prod) {
+            g.at.prod_rpb = p.rows_per_block;
+            g.at.prod_blocks = (int)nblk;
+        }
+        if (!placed && p.prod) {
+            g.at.first = (int)begin;
+            begin += (unsigned)g.at.blocks;
+            placed = true;
+        }
     }
     return begin;
 }
@@ -767,7 +964,7 @@ static hipError_t launch_group_x(hipStream_t s, int x_dtype, StreamGroup& g, siz
     }
 }
 
-// Key splits of the carried attention: enough workgroups to spread the cache
+// Key splits of a decode attention: enough workgroups to spread the cache
 // reads over the device (heads * splits ~ CUs), each split a whole number of
 // workgroup iterations (NWAVE waves x ATTN_NL loads x keys per load).
 static void attn_split(int heads, int D, int seq_kv, int num_cus, int* splits, int* keys_per_split) {
@@ -780,6 +977,8 @@ static void attn_split(int heads, int D, int seq_kv, int num_cus, int* splits, i
     *splits = (seq_kv + k - 1) / k;
 }
 
+static int attn_seq(const StreamAttnDesc& d) { return d.cached + (d.step ? 1 : 0); }
+
 size_t stream_attn_workspace_bytes(int heads, int head_dim, int seq_kv, int num_cus) {
     if (heads < 1 || (head_dim != 64 && head_dim != 128) || seq_kv < 1) return 0;
     int splits = 1, kps = 0;
@@ -787,43 +986,71 @@ size_t stream_attn_workspace_bytes(int heads, int head_dim, int seq_kv, int num_
     return ((size_t)heads * splits * head_dim * 4 + 15) / 16 * 16 + (size_t)heads * splits * 8;
 }
 
-// Fills g.at and moves the problems that read o to the end of the group
-// (marked dep).  False when the launch cannot carry the attention.
-static bool attach_attention(StreamGroup& g, const StreamAttnDesc& d, int x_dtype, int M, int num_cus,
-                             size_t& lds) {
-    if (M != 1 || x_dtype != MVLM_F32 || (d.head_dim != 64 && d.head_dim != 128) || d.heads < 1 ||
-        d.heads > ATTN_MAX_HEADS || d.seq_kv < 1 || !d.q || !d.k || !d.v || !d.o || !d.sync || !d.workspace)
+// The device-side description of attention `d` (no problems attached).
+static bool attn_fill(StreamAttn& a, const StreamAttnDesc& d, int num_cus) {
+    const int seq = attn_seq(d);
+    if ((d.head_dim != 64 && d.head_dim != 128) || d.heads < 1 || d.heads > ATTN_MAX_HEADS || seq < 1 ||
+        d.cached < 0 || !d.k || !d.v || !d.o || !d.workspace || (d.step ? !d.qkv : !d.q) || (d.mode == 1 && !d.step))
         return false;
-    if ((int64_t)d.seq_kv * d.heads * d.head_dim * 2 > (int64_t)1 << 31) return false;
-    StreamAttn& a = g.at;
+    if ((int64_t)(d.cached + 1) * d.heads * d.head_dim * 2 > (int64_t)1 << 31) return false;
+    a = StreamAttn{};
     a.q = (const uint16_t*)d.q;
-    a.k = (const uint16_t*)d.k;
-    a.v = (const uint16_t*)d.v;
+    a.qkv = (const float*)d.qkv;
+    a.k = (uint16_t*)d.k;
+    a.v = (uint16_t*)d.v;
     a.o = d.o;
     a.sync = (uint8_t*)d.sync;
     a.heads = d.heads;
     a.D = d.head_dim;
-    a.seq_kv = d.seq_kv;
-    attn_split(d.heads, d.head_dim, d.seq_kv, num_cus, &a.splits, &a.keys_per_split);
+    a.cached = d.cached;
+    a.seq_kv = seq;
+    a.mode = d.mode;
+    a.step = d.step ? 1 : 0;
+    attn_split(d.heads, d.head_dim, seq, num_cus, &a.splits, &a.keys_per_split);
     a.part_o = (float*)d.workspace;
-    a.part_ml = a.part_o + ((size_t)d.heads * a.splits * d.head_dim + 3) / 4 * 4;
+    a.part_ml = a.part_o + (size_t)d.heads * a.splits * d.head_dim;
     a.blocks = d.heads * a.splits;
     a.scale_log2 = d.scale * 1.4426950408889634f;
+    return a.blocks <= ATTN_MAX_BLOCKS;
+}
+
+// Fills g.at and orders the problems for the mode: mode 0 moves the problems
+// that read o to the end (dep); mode 1 moves the problem whose fp32 output is
+// qkv (N = 3 heads D) to the front (prod).  False when the launch cannot
+// carry the attention.
+static bool attach_attention(StreamGroup& g, const StreamAttnDesc& d, int x_dtype, int M, int num_cus,
+                             size_t& lds) {
+    if (M != 1 || !d.sync || !attn_fill(g.at, d, num_cus)) return false;
+    g.at.merge = 1;
     StreamProblem sorted[MAX_GROUP];
     int n = 0;
-    for (int pass = 0; pass < 2; ++pass)
+    if (d.mode == 0) {
+        if (x_dtype != MVLM_F32) return false;
+        for (int pass = 0; pass < 2; ++pass)
+            for (int i = 0; i < g.count; ++i)
+                if ((g.p[i].x == (const void*)d.o) == (pass == 1)) {
+                    sorted[n] = g.p[i];
+                    sorted[n++].dep = pass;
+                }
+        if (sorted[g.count - 1].dep == 0) return false;   // nothing reads o
         for (int i = 0; i < g.count; ++i)
-            if ((g.p[i].x == (const void*)d.o) == (pass == 1)) {
-                sorted[n] = g.p[i];
-                sorted[n++].dep = pass;
-            }
-    if (sorted[g.count - 1].dep == 0) return false;   // nothing reads o
-    for (int i = 0; i < g.count; ++i) {
-        if (sorted[i].dep && !kDepShape[sorted[i].shape]) return false;
-        g.p[i] = sorted[i];
+            if (sorted[i].dep && !kDepShape[sorted[i].shape]) return false;
+    } else {
+        int pi = -1;
+        for (int i = 0; i < g.count; ++i) {
+            if (g.p[i].y != d.qkv) continue;
+            if (pi >= 0 || g.p[i].y_dtype != MVLM_F32 || g.p[i].N != 3 * d.heads * d.head_dim) return false;
+            pi = i;
+        }
+        if (pi < 0 || !kDepShape[g.p[pi].shape]) return false;
+        sorted[n] = g.p[pi];
+        sorted[n++].prod = 1;
+        for (int i = 0; i < g.count; ++i)
+            if (i != pi) sorted[n++] = g.p[i];
     }
+    for (int i = 0; i < g.count; ++i) g.p[i] = sorted[i];
     lds = std::max(lds, (size_t)NWAVE * (d.head_dim + 2) * 4);
-    return true;
+    return lds <= STREAM_LDS_MAX;
 }
 
 template <class F>
@@ -837,8 +1064,10 @@ static hipError_t attn_capacity(StreamGroup& g, size_t lds, int num_cus) {
         e != hipSuccess)
         return e;
     partition(g);
-    return g.at.consumers < per_cu * num_cus && g.at.consumers <= ATTN_MAX_CONSUMERS ? hipSuccess
-                                                                                   : hipErrorInvalidConfiguration;
+    const int waiting = g.at.mode == 0 ? g.at.consumers : g.at.blocks;
+    const bool fits = g.at.mode == 0 ? g.at.consumers <= ATTN_MAX_CONSUMERS
+                                     : g.at.prod_blocks <= ATTN_MAX_PRODUCERS && g.at.prod_blocks > 0;
+    return waiting < per_cu * num_cus && fits ? hipSuccess : hipErrorInvalidConfiguration;
 }
 
 static hipError_t build_group(StreamGroup& g, size_t& lds, int count, const void* const* xs, int x_dtype,
@@ -846,12 +1075,10 @@ static hipError_t build_group(StreamGroup& g, size_t& lds, int count, const void
                               const Epilogue* eps, int M);
 
 hipError_t stream_attn_check(int count, const void* const* xs, int x_dtype, const mvlm_weight* const* ws,
-                             const StreamAttnDesc& at, int num_cus) {
+                             void* const* ys, const int* y_dtypes, const StreamAttnDesc& at, int num_cus) {
     StreamGroup g{};
     size_t lds = 0;
-    std::vector<void*> ys(count > 0 ? count : 1, nullptr);
-    std::vector<int> yd(count > 0 ? count : 1, MVLM_F32);
-    if (const hipError_t e = build_group(g, lds, count, xs, x_dtype, ws, ys.data(), yd.data(), num_cus, nullptr, 1);
+    if (const hipError_t e = build_group(g, lds, count, xs, x_dtype, ws, ys, y_dtypes, num_cus, nullptr, 1);
         e != hipSuccess)
         return e;
     if (!attach_attention(g, at, x_dtype, 1, num_cus, lds)) return hipErrorInvalidValue;
@@ -863,6 +1090,27 @@ hipError_t stream_attn_check(int count, const void* const* xs, int x_dtype, cons
         case MVLM_BF16: return attn_capacity<DenseFmt<__hip_bfloat16>>(g, lds, num_cus);
         default: return hipErrorInvalidValue;
     }
+}
+
+// A decode attention as launches of its own: the split kernel, then (more
+// than one split) the merge kernel.
+hipError_t launch_attn_decode(hipStream_t s, const StreamAttnDesc& d, int num_cus) {
+    StreamAttn a;
+    if (!attn_fill(a, d, num_cus > 0 ? num_cus : 256)) return hipErrorInvalidValue;
+    a.merge = 0;
+    const bool two = a.splits > 1;
+    if (!two) {
+        if (a.D == 64) launch_kernel(attn_split_kernel<64>, dim3(a.blocks), dim3(64 * NWAVE), 0, s, a);
+        else launch_kernel(attn_split_kernel<128>, dim3(a.blocks), dim3(64 * NWAVE), 0, s, a);
+    } else {
+        if (a.D == 64)
+            launch_kernel_part(LaunchPart::First, attn_split_kernel<64>, dim3(a.blocks), dim3(64 * NWAVE), 0, s, a);
+        else
+            launch_kernel_part(LaunchPart::First, attn_split_kernel<128>, dim3(a.blocks), dim3(64 * NWAVE), 0, s, a);
+        if (a.D == 64) launch_kernel_part(LaunchPart::Last, attn_merge_kernel<64>, dim3(a.heads), dim3(64), 0, s, a);
+        else launch_kernel_part(LaunchPart::Last, attn_merge_kernel<128>, dim3(a.heads), dim3(64), 0, s, a);
+    }
+    return hipGetLastError();
 }
 
 // The launch's problems (validated by the caller) and its LDS bytes.

@@ -16,7 +16,8 @@ using namespace mvlm;
 
 namespace {
 
-enum OpKind { OP_GEMM_NAIVE, OP_GEMM_TILED, OP_GEMV_EXACT, OP_GEMM_MFMA, OP_GEMV_DENSE, OP_GEMV_QUANT, OP_GEMV_GROUP, OP_ATTENTION, OP_ARGMAX };
+enum OpKind { OP_GEMM_NAIVE, OP_GEMM_TILED, OP_GEMV_EXACT, OP_GEMM_MFMA, OP_GEMV_DENSE, OP_GEMV_QUANT, OP_GEMV_GROUP, OP_ATTENTION,
+              OP_ATTN_STEP, OP_ARGMAX };
 
 struct Op {
     OpKind kind;
@@ -43,13 +44,20 @@ struct Op {
     float scale = 0.0f;
     void* workspace = nullptr;    // attention key splits, GEMM K splits
     size_t workspace_bytes = 0;
-    // grouped GEMV of a plan that can also compute the decode attention added
-    // just before it (whose output some entries read as x): plan fusion
-    bool attn_fusable = false;
+    // plan fusion: a grouped GEMV whose launch can also compute a decode
+    // attention entry next to it; 1: the entry before it (some entries read
+    // its output as x), 2: the entry after it (a decode step whose q, k, v
+    // one entry writes)
+    int attn_carry = 0;
     StreamAttnDesc attn;
 };
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
+    const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+    return a && b && an && bn && x < y + bn && y < x + an;
+}
 
 int need(const mvlm_buffer* b, size_t bytes, const char* fn, const char* name) {
     if (b->bytes < bytes)
@@ -215,6 +223,48 @@ int make_attention(mvlm_device* dev, const mvlm_buffer* Q, const mvlm_buffer* K,
     return device_scratch(dev, op->workspace_bytes, &op->workspace);
 }
 
+// Decode attention step (mode 1 of StreamAttnDesc): qkv fp32 [3][heads][D],
+// caches fp16 [cached + 1][heads][D] (row `cached` written), O fp32 [heads][D].
+int make_attn_step(mvlm_device* dev, const mvlm_buffer* qkv, mvlm_buffer* Kc, mvlm_buffer* Vc, mvlm_buffer* O,
+                   int cached, int heads, int head_dim, float scale, const char* fn, Op* op) {
+    REQUIRE(dev && qkv && Kc && Vc && O, "%s: null argument", fn);
+    REQUIRE(qkv->dev == dev && Kc->dev == dev && Vc->dev == dev && O->dev == dev,
+            "%s: buffers belong to another device", fn);
+    REQUIRE(cached >= 0 && heads > 0 && head_dim > 0, "%s: cached=%d num_heads=%d head_dim=%d", fn, cached, heads,
+            head_dim);
+    REQUIRE(scale >= 0.0f && scale < INFINITY, "%s: scale %g must be finite and non-negative", fn, (double)scale);
+    if (head_dim != 64 && head_dim != 128)
+        return set_error(MVLM_ERR_UNSUPPORTED, "%s: head_dim=%d is not 64 or 128", fn, head_dim);
+    if (heads > 192 || (int64_t)(cached + 1) * heads * head_dim * 2 > ((int64_t)1 << 31))
+        return set_error(MVLM_ERR_UNSUPPORTED, "%s: more than 192 heads or a cache over 2 GiB", fn);
+    REQUIRE(aligned16(qkv->ptr) && aligned16(Kc->ptr) && aligned16(Vc->ptr) && aligned16(O->ptr),
+            "%s: qkv, K_cache, V_cache and O must be 16-byte aligned", fn);
+    const size_t row = (size_t)heads * head_dim;
+    NEED(qkv, 3 * row * 4, "qkv");
+    NEED(Kc, ((size_t)cached + 1) * row * 2, "K_cache");
+    NEED(Vc, ((size_t)cached + 1) * row * 2, "V_cache");
+    NEED(O, row * 4, "O");
+    REQUIRE(!(overlaps(Kc->ptr, Kc->bytes, Vc->ptr, Vc->bytes) || overlaps(O->ptr, row * 4, qkv->ptr, 3 * row * 4) ||
+              overlaps(O->ptr, row * 4, Kc->ptr, Kc->bytes) || overlaps(O->ptr, row * 4, Vc->ptr, Vc->bytes)),
+            "%s: K_cache, V_cache and O must not overlap each other or qkv", fn);
+    op->kind = OP_ATTN_STEP;
+    op->a = qkv->ptr; op->b = Kc->ptr; op->v = Vc->ptr; op->c = O->ptr;
+    op->c_dtype = MVLM_F32;
+    op->N = cached; op->batch = heads; op->K = head_dim;
+    op->scale = scale == 0.0f ? 1.0f / sqrtf((float)head_dim) : scale;
+    op->num_cus = dev->prop.multiProcessorCount;
+    op->workspace_bytes = stream_attn_workspace_bytes(heads, head_dim, cached + 1, op->num_cus);
+    return device_scratch(dev, op->workspace_bytes, &op->workspace);
+}
+
+static StreamAttnDesc attn_step_desc(const Op& op) {
+    StreamAttnDesc d;
+    d.qkv = op.a; d.k = const_cast<void*>(op.b); d.v = const_cast<void*>(op.v); d.o = (float*)op.c;
+    d.heads = op.batch; d.head_dim = op.K; d.cached = op.N; d.mode = 1; d.step = 1; d.scale = op.scale;
+    d.workspace = op.workspace;
+    return d;
+}
+
 int make_argmax(mvlm_device* dev, const mvlm_buffer* x, int dtype, int rows, int n, int64_t ld,
                 mvlm_buffer* out, const char* fn, Op* op) {
     REQUIRE(dev && x && out, "%s: null argument", fn);
@@ -375,6 +425,8 @@ hipError_t enqueue_op(hipStream_t s, const Op& op, bool with_attn = false) {
         case OP_ATTENTION:
             return launch_attention(s, op.a, op.b, op.v, op.c, op.c_dtype, op.M, op.N, op.batch, op.K, op.causal,
                                     op.scale, op.num_cus, op.workspace, op.workspace_bytes);
+        case OP_ATTN_STEP:
+            return launch_attn_decode(s, attn_step_desc(op), op.num_cus);
     }
     return hipErrorInvalidValue;
 }
@@ -549,6 +601,13 @@ extern "C" int mvlm_attention_decode(mvlm_device* dev, const mvlm_buffer* Q, con
                        &op));
 }
 
+extern "C" int mvlm_attention_decode_step(mvlm_device* dev, const mvlm_buffer* qkv, mvlm_buffer* K_cache,
+                                          mvlm_buffer* V_cache, mvlm_buffer* O, int cached, int num_heads,
+                                          int head_dim, float scale, mvlm_event** ev) {
+    const char* fn = __func__;
+    RUN(make_attn_step(dev, qkv, K_cache, V_cache, O, cached, num_heads, head_dim, scale, fn, &op));
+}
+
 extern "C" int mvlm_argmax(mvlm_device* dev, const mvlm_buffer* x, int dtype, int rows, int n, int64_t ld,
                            mvlm_buffer* out_index, mvlm_event** ev) {
     const char* fn = __func__;
@@ -599,52 +658,16 @@ extern "C" int mvlm_plan_destroy(mvlm_plan* plan) {
 
 extern "C" int mvlm_plan_size(const mvlm_plan* plan) { return plan ? (int)plan->ops.size() : MVLM_ERR_INVALID_ARG; }
 
-static bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
-    const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
-    return a && b && an && bn && x < y + bn && y < x + an;
-}
-
-// A grouped M = 1 GEMV pushed right after a decode attention (one query,
-// fp32 output, head_dim 64 or 128) that some entries read as x can carry that
-// attention in its own launch.  The entries must not write the attention's
-// inputs or output, nor read its output other than as x, and the launch must
-// fit the fused kernel (stream_attn_check).  Marks op and gives it the
-// attention's description; the plan then skips the attention launch while
-// fusion is on.
-static void mark_fusable(mvlm_plan* plan, Op& op) {
-    if (op.kind != OP_GEMV_GROUP || op.M != 1 || op.a_dtype != MVLM_F32 || plan->ops.empty()) return;
-    const Op& a = plan->ops.back();
-    if (a.kind != OP_ATTENTION || a.M != 1 || a.c_dtype != MVLM_F32 || (a.K != 64 && a.K != 128)) return;
-    const size_t q_bytes = (size_t)a.batch * a.K * 2, kv_bytes = (size_t)a.N * a.batch * a.K * 2;
-    const size_t o_bytes = (size_t)a.batch * a.K * 4;
-    bool reads_o = false;
-    for (int i = 0; i < op.gcount; ++i) {
-        const mvlm_weight* w = op.gw[i];
-        const size_t y_bytes = (size_t)w->N * dtype_size(op.gyd[i]);
-        if (overlaps(op.gy[i], y_bytes, a.a, q_bytes) || overlaps(op.gy[i], y_bytes, a.b, kv_bytes) ||
-            overlaps(op.gy[i], y_bytes, a.v, kv_bytes) || overlaps(op.gy[i], y_bytes, a.c, o_bytes))
-            return;
-        if (op.gx[i] == a.c) reads_o = true;
-        else if (overlaps(op.gx[i], (size_t)w->K * 4, a.c, o_bytes)) return;
-        const Epilogue& e = op.gep[i];
-        const size_t eb = (size_t)w->N * dtype_size(e.dtype);
-        if (overlaps(e.bias, eb, a.c, o_bytes) || overlaps(e.mul, eb, a.c, o_bytes) || overlaps(e.res, eb, a.c, o_bytes))
-            return;
-    }
-    if (!reads_o) return;
-    StreamAttnDesc d;
-    d.q = a.a; d.k = a.b; d.v = a.v; d.o = (float*)a.c;
-    d.heads = a.batch; d.head_dim = a.K; d.seq_kv = a.N; d.scale = a.scale;
+// Gives op (a grouped GEMV) attention d with a zeroed sync area of its own,
+// if the launch can carry it (stream_attn_check).
+static bool attach_sync(mvlm_plan* plan, Op& op, StreamAttnDesc d) {
     mvlm_device* dev = plan->dev;
-    if (device_scratch(dev, stream_attn_workspace_bytes(d.heads, d.head_dim, d.seq_kv, op.num_cus), &d.workspace) !=
-        MVLM_OK)
-        return;
     if (hipSetDevice(dev->ordinal) != hipSuccess || hipMalloc(&d.sync, SYNC_BYTES) != hipSuccess) {
         (void)hipGetLastError();
-        return;
+        return false;
     }
     bool ok = hipMemset(d.sync, 0, SYNC_BYTES) == hipSuccess &&
-              stream_attn_check(op.gcount, op.gx, op.a_dtype, op.gw, d, op.num_cus) == hipSuccess;
+              stream_attn_check(op.gcount, op.gx, op.a_dtype, op.gw, op.gy, op.gyd, d, op.num_cus) == hipSuccess;
     if (ok) {
         try {
             plan->sync_areas.push_back(d.sync);
@@ -655,15 +678,109 @@ static void mark_fusable(mvlm_plan* plan, Op& op) {
     if (!ok) {
         (void)hipGetLastError();
         (void)hipFree(d.sync);
-        return;
+        return false;
     }
     op.attn = d;
-    op.attn_fusable = true;
+    return true;
+}
+
+// A grouped M = 1 GEMV pushed right after a decode attention (OP_ATTENTION
+// with one query, fp32 output, head_dim 64 or 128; or OP_ATTN_STEP) that
+// some entries read as x can carry that attention in its own launch, ahead of
+// those entries.  The entries must not write the attention's inputs or
+// output, nor read its output other than as x (nor, for a step, the caches),
+// and the launch must fit the fused kernel (stream_attn_check).  Marks op and
+// gives it the attention's description; the plan then skips the attention
+// launch while fusion is on.  A step already carried by the GEMV before it
+// moves here: measured, waiting readers cost less than a waiting attention.
+static void mark_fusable(mvlm_plan* plan, Op& op) {
+    if (op.kind != OP_GEMV_GROUP || op.M != 1 || op.a_dtype != MVLM_F32 || plan->ops.empty()) return;
+    const Op& a = plan->ops.back();
+    const bool step = a.kind == OP_ATTN_STEP;
+    if (!step && (a.kind != OP_ATTENTION || a.M != 1 || a.c_dtype != MVLM_F32 || (a.K != 64 && a.K != 128))) return;
+    const size_t row = (size_t)a.batch * a.K;
+    const size_t in_bytes = step ? 3 * row * 4 : row * 2;                       // qkv or q
+    const size_t kv_bytes = ((size_t)a.N + (step ? 1 : 0)) * row * 2;
+    const size_t o_bytes = row * 4;
+    bool reads_o = false;
+    for (int i = 0; i < op.gcount; ++i) {
+        const mvlm_weight* w = op.gw[i];
+        const size_t y_bytes = (size_t)w->N * dtype_size(op.gyd[i]);
+        if (overlaps(op.gy[i], y_bytes, a.a, in_bytes) || overlaps(op.gy[i], y_bytes, a.b, kv_bytes) ||
+            overlaps(op.gy[i], y_bytes, a.v, kv_bytes) || overlaps(op.gy[i], y_bytes, a.c, o_bytes))
+            return;
+        const size_t x_bytes = (size_t)w->K * 4;
+        if (op.gx[i] == a.c) reads_o = true;
+        else if (overlaps(op.gx[i], x_bytes, a.c, o_bytes)) return;
+        const Epilogue& e = op.gep[i];
+        const size_t eb = (size_t)w->N * dtype_size(e.dtype);
+        for (const void* in : {(const void*)e.bias, e.mul, e.res})
+            if (overlaps(in, eb, a.c, o_bytes)) return;
+        if (step)   // the step writes cache row `cached`: no entry may read the caches
+            for (const void* in : {op.gx[i], (const void*)e.bias, e.mul, e.res}) {
+                const size_t nb = in == op.gx[i] ? x_bytes : eb;
+                if (overlaps(in, nb, a.b, kv_bytes) || overlaps(in, nb, a.v, kv_bytes)) return;
+            }
+    }
+    if (!reads_o) return;
+    StreamAttnDesc d;
+    if (step) {
+        d = attn_step_desc(a);
+    } else {
+        d.q = a.a; d.k = const_cast<void*>(a.b); d.v = const_cast<void*>(a.v); d.o = (float*)a.c;
+        d.heads = a.batch; d.head_dim = a.K; d.cached = a.N; d.scale = a.scale;
+        if (device_scratch(plan->dev, stream_attn_workspace_bytes(d.heads, d.head_dim, d.cached, op.num_cus),
+                           &d.workspace) != MVLM_OK)
+            return;
+    }
+    d.mode = 0;
+    if (!attach_sync(plan, op, d)) return;
+    op.attn_carry = 1;
+    if (step && plan->ops.size() >= 2 && plan->ops[plan->ops.size() - 2].attn_carry == 2)
+        plan->ops[plan->ops.size() - 2].attn_carry = 0;   // no longer carried by the producer's launch
+}
+
+// A decode attention step (OP_ATTN_STEP) pushed right after a grouped M = 1
+// GEMV one of whose entries writes its qkv (fp32, N = 3 heads D) can run in
+// that GEMV's launch, after that entry's rows.  The other entries must not
+// write qkv, the caches or O, and no entry may read the caches or O (the
+// step writes cache row `cached` and O).  Marks the GEMV entry.
+static void mark_fusable_after(mvlm_plan* plan, const Op& a) {
+    if (a.kind != OP_ATTN_STEP || plan->ops.empty()) return;
+    Op& op = plan->ops.back();
+    if (op.kind != OP_GEMV_GROUP || op.M != 1 || op.attn_carry != 0) return;
+    const size_t row = (size_t)a.batch * a.K;
+    const size_t kv_bytes = ((size_t)a.N + 1) * row * 2;
+    int producers = 0;
+    for (int i = 0; i < op.gcount; ++i) {
+        const mvlm_weight* w = op.gw[i];
+        const size_t y_bytes = (size_t)w->N * dtype_size(op.gyd[i]);
+        const size_t x_bytes = (size_t)w->K * dtype_size(op.a_dtype);
+        if (op.gy[i] == a.a && op.gyd[i] == MVLM_F32 && (size_t)w->N == 3 * row) {
+            ++producers;
+        } else if (overlaps(op.gy[i], y_bytes, a.a, 3 * row * 4)) {
+            return;
+        }
+        if (overlaps(op.gy[i], y_bytes, a.b, kv_bytes) || overlaps(op.gy[i], y_bytes, a.v, kv_bytes) ||
+            overlaps(op.gy[i], y_bytes, a.c, row * 4))
+            return;
+        const Epilogue& e = op.gep[i];
+        const size_t eb = (size_t)w->N * dtype_size(e.dtype);
+        for (const void* in : {op.gx[i], e.bias, e.mul, e.res}) {
+            const size_t nb = in == op.gx[i] ? x_bytes : eb;
+            if (overlaps(in, nb, a.b, kv_bytes) || overlaps(in, nb, a.v, kv_bytes) || overlaps(in, nb, a.c, row * 4))
+                return;
+        }
+    }
+    if (producers != 1) return;
+    StreamAttnDesc d = attn_step_desc(a);
+    if (attach_sync(plan, op, d)) op.attn_carry = 2;
 }
 
 static int plan_push(mvlm_plan* plan, Op op) {
     drop_graph(plan);   // a recorded graph no longer matches
     mark_fusable(plan, op);
+    mark_fusable_after(plan, op);
     try {
         plan->ops.push_back(op);
     } catch (...) {
@@ -769,6 +886,16 @@ extern "C" int mvlm_plan_add_attention(mvlm_plan* plan, const mvlm_buffer* Q, co
     return st != MVLM_OK ? st : plan_push(plan, op);
 }
 
+extern "C" int mvlm_plan_add_attention_decode_step(mvlm_plan* plan, const mvlm_buffer* qkv, mvlm_buffer* K_cache,
+                                                   mvlm_buffer* V_cache, mvlm_buffer* O, int cached, int num_heads,
+                                                   int head_dim, float scale) {
+    const char* fn = __func__;
+    REQUIRE(plan, "%s: null argument", fn);
+    Op op{};
+    int st = make_attn_step(plan->dev, qkv, K_cache, V_cache, O, cached, num_heads, head_dim, scale, fn, &op);
+    return st != MVLM_OK ? st : plan_push(plan, op);
+}
+
 extern "C" int mvlm_plan_add_argmax(mvlm_plan* plan, const mvlm_buffer* x, int dtype, int rows, int n, int64_t ld,
                                     mvlm_buffer* out_index) {
     const char* fn = __func__;
@@ -778,19 +905,21 @@ extern "C" int mvlm_plan_add_argmax(mvlm_plan* plan, const mvlm_buffer* x, int d
     return st != MVLM_OK ? st : plan_push(plan, op);
 }
 
-// Whether entry i is launched by entry i + 1 (a decode attention carried by
-// the grouped GEMV after it) and whether entry i carries entry i - 1.
-static bool carried_by_next(const mvlm_plan* plan, size_t i) {
-    return plan->fuse && i + 1 < plan->ops.size() && plan->ops[i + 1].attn_fusable;
+// Whether entry i is launched by a neighbour (a decode attention carried by
+// the grouped GEMV after it, or a decode step by the one before it) and
+// whether entry i carries a neighbour.
+static bool carried(const mvlm_plan* plan, size_t i) {
+    return plan->fuse && ((i + 1 < plan->ops.size() && plan->ops[i + 1].attn_carry == 1) ||
+                          (i > 0 && plan->ops[i - 1].attn_carry == 2));
 }
-static bool carries_prev(const mvlm_plan* plan, size_t i) { return plan->fuse && plan->ops[i].attn_fusable; }
+static bool carries(const mvlm_plan* plan, size_t i) { return plan->fuse && plan->ops[i].attn_carry != 0; }
 
 // The plan's launches in order: one per entry, except attention entries
 // carried by the next entry's launch.
 static int enqueue_all(mvlm_plan* plan) {
     for (size_t i = 0; i < plan->ops.size(); ++i) {
-        if (carried_by_next(plan, i)) continue;
-        const hipError_t e = enqueue_op(plan->dev->stream, plan->ops[i], carries_prev(plan, i));
+        if (carried(plan, i)) continue;
+        const hipError_t e = enqueue_op(plan->dev->stream, plan->ops[i], carries(plan, i));
         if (e != hipSuccess) return check_hip(e, "plan launch");
     }
     return MVLM_OK;
@@ -806,7 +935,7 @@ extern "C" int mvlm_plan_set_fusion(mvlm_plan* plan, int enable) {
 extern "C" int mvlm_plan_fused(const mvlm_plan* plan) {
     if (!plan) return MVLM_ERR_INVALID_ARG;
     int n = 0;
-    for (size_t i = 0; i < plan->ops.size(); ++i) n += carries_prev(plan, i) ? 1 : 0;
+    for (size_t i = 0; i < plan->ops.size(); ++i) n += carries(plan, i) ? 1 : 0;
     return n;
 }
 
@@ -817,7 +946,7 @@ extern "C" int mvlm_plan_check(mvlm_plan* plan) {
     HIP_TRY(hipStreamSynchronize(dev->stream));
     int failed = 0;
     for (const Op& op : plan->ops) {
-        if (!op.attn_fusable) continue;
+        if (!op.attn_carry) continue;
         uint32_t err = 0;
         HIP_TRY(hipMemcpy(&err, (const char*)op.attn.sync + SYNC_ERR_OFFSET, 4, hipMemcpyDeviceToHost));
         if (!err) continue;
@@ -878,10 +1007,10 @@ extern "C" int mvlm_plan_profile(mvlm_plan* plan, float* op_ms, int capacity) {
     int launched = 0;
     int last = -1;
     for (int i = 0; i < n && st == MVLM_OK; ++i) {
-        if (carried_by_next(plan, (size_t)i)) continue;   // timed with the launch that carries it
+        if (carried(plan, (size_t)i)) continue;   // timed with the launch that carries it
         t.start = ev[2 * i];
         t.stop = ev[2 * i + 1];
-        const hipError_t e = enqueue_op(s, plan->ops[i], carries_prev(plan, (size_t)i));
+        const hipError_t e = enqueue_op(s, plan->ops[i], carries(plan, (size_t)i));
         t = KernelTiming{};
         if (e != hipSuccess) st = check_hip(e, "plan launch");
         else last = i;
@@ -891,7 +1020,7 @@ extern "C" int mvlm_plan_profile(mvlm_plan* plan, float* op_ms, int capacity) {
     if (st == MVLM_OK && launched > 0)
         st = check_hip(hipEventSynchronize(ev[2 * (size_t)(launched - 1) + 1]), "hipEventSynchronize");
     for (int i = 0; i < n && st == MVLM_OK; ++i) {
-        if (carried_by_next(plan, (size_t)i)) op_ms[i] = 0.0f;
+        if (carried(plan, (size_t)i)) op_ms[i] = 0.0f;
         else st = check_hip(hipEventElapsedTime(&op_ms[i], ev[2 * i], ev[2 * i + 1]), "hipEventElapsedTime");
     }
     for (hipEvent_t e : ev)

@@ -144,6 +144,8 @@ _SIGNATURES = {
     "mvlm_plan_run": (c_int, [_P, c_int, _PP]),
     "mvlm_plan_profile": (c_int, [_P, POINTER(c_float), c_int]),
     "mvlm_plan_set_fusion": (c_int, [_P, c_int]),
+    "mvlm_attention_decode_step": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_float, _PP]),
+    "mvlm_plan_add_attention_decode_step": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_float]),
     "mvlm_plan_fused": (c_int, [_P]),
     "mvlm_plan_check": (c_int, [_P]),
     "mvlm_marker_record": (c_int, [_P, _PP]),
@@ -485,6 +487,12 @@ class Plan:
         self._keep += [Q, K, V, O]
         return self
 
+    def add_attention_decode_step(self, qkv, K_cache, V_cache, O, cached, num_heads, head_dim, scale=0.0):
+        _call("mvlm_plan_add_attention_decode_step", self.handle, qkv.handle, K_cache.handle, V_cache.handle,
+              O.handle, cached, num_heads, head_dim, scale)
+        self._keep += [qkv, K_cache, V_cache, O]
+        return self
+
     def add_argmax(self, x, dtype, rows, n, ld, out_index):
         _call("mvlm_plan_add_argmax", self.handle, x.handle, dtype, rows, n, ld, out_index.handle)
         self._keep += [x, out_index]
@@ -688,6 +696,11 @@ class Device:
     def attention_decode(self, Q, K_cache, V_cache, O, cache_len, num_heads, head_dim, event=False):
         return self._launch("mvlm_attention_decode", (Q.handle, K_cache.handle, V_cache.handle, O.handle, cache_len,
                                                       num_heads, head_dim), event)
+
+    def attention_decode_step(self, qkv, K_cache, V_cache, O, cached, num_heads, head_dim, scale=0.0, event=False):
+        """Append the new key/value of qkv (fp32 q | k | v) to row `cached` of the fp16 caches, then attend."""
+        return self._launch("mvlm_attention_decode_step", (qkv.handle, K_cache.handle, V_cache.handle, O.handle,
+                                                           cached, num_heads, head_dim, scale), event)
 
     def argmax(self, x, dtype, rows, n, ld, out_index, event=False):
         """out_index[r] (int32 on the device) = first index of the largest key of row r."""

@@ -82,8 +82,10 @@ def test_decode_step_plan_outputs(dev, orc, qt, M):
 @pytest.mark.parametrize("qt,cache,fuse", [("q8_0", 512, True), ("q8_0", 512, False), ("q4_0", 2048, True)])
 def test_decode_token_plan_picks_the_argmax(dev, orc, qt, cache, fuse):
     """The token plan end to end: every GEMV output (dense on the attention
-    output the plan computed), the attention output against the oracle's
-    fp64 attention (the attention tests' bound), and the token pick."""
+    output the plan computed), the attention step of the first and last layer
+    (the cache append bit for bit, the output against the oracle's fp64
+    attention over cache + 1 keys, the attention tests' bound), and the token
+    pick."""
     print(f"[token plan] {qt} cache {cache} fuse={fuse}", flush=True)
     plan, weights, io = bench.build_token_plan(dev, m, qt, cache, fuse)
     assert len(plan) == 24 * 3 + 2
@@ -93,13 +95,19 @@ def test_decode_token_plan_picks_the_argmax(dev, orc, qt, cache, fuse):
     plan.check()
     check_outputs(dev, orc, weights, io, 1)
     H, D = 32, 64
-    q = io["q"].download(np.uint16, H * D).reshape(1, H, D)
-    k = io["k"].download(np.uint16, cache * H * D).reshape(cache, H, D)
-    v = io["v"].download(np.uint16, cache * H * D).reshape(cache, H, D)
-    O64, A, R = orc.attention_f64(q, k, v, 1, cache, H, D, False, 1.0 / np.sqrt(D))
-    got = io["o"].download(np.float32, H * D).astype(np.float64).reshape(1, H, D)
-    tol = (2.0 ** -10 + cache * 2.0 ** -24 + 2 * D * 2.0 ** -24 * R[..., None]) * A + np.abs(O64) * 2.0 ** -24 + 1e-12
-    assert np.all(np.abs(got - O64) <= tol)
+    HD = H * D
+    for layer in (0, 23):
+        qkv = io["y"][4 * layer].download(np.float32, 3 * HD)
+        q = np.asarray(qkv[:HD], np.float16).view(np.uint16).reshape(1, H, D)
+        kc = io["kc"][layer].download(np.uint16, (cache + 1) * HD).reshape(cache + 1, H, D)
+        vc = io["vc"][layer].download(np.uint16, (cache + 1) * HD).reshape(cache + 1, H, D)
+        assert np.array_equal(kc[cache], np.asarray(qkv[HD:2 * HD], np.float16).view(np.uint16).reshape(H, D))
+        assert np.array_equal(vc[cache], np.asarray(qkv[2 * HD:], np.float16).view(np.uint16).reshape(H, D))
+        O64, A, R = orc.attention_f64(q, kc, vc, 1, cache + 1, H, D, False, 1.0 / np.sqrt(D))
+        got = io["o"][layer].download(np.float32, HD).astype(np.float64).reshape(1, H, D)
+        tol = ((2.0 ** -10 + (cache + 1) * 2.0 ** -24 + 2 * D * 2.0 ** -24 * R[..., None]) * A
+               + np.abs(O64) * 2.0 ** -24 + 1e-12)
+        assert np.all(np.abs(got - O64) <= tol), layer
     logits = io["y"][-1].download(np.float32, 51200)
     want = orc.argmax(logits, m.F32, 1, 51200, 51200)[0]
     assert int(io["token"].download(np.int32, 1)[0]) == int(want)

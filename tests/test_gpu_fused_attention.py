@@ -216,3 +216,188 @@ def test_long_rows_reading_o_are_not_fused(dev):
     p.check()
     p.destroy()
     W.free()
+
+
+# ---- decode attention step: q, k, v from a fused QKV projection's output -----
+
+def f16_round(x):
+    return np.asarray(x, np.float32).astype(np.float16)
+
+
+class StepCase:
+    """group {x -> Wqkv -> qkv (N = 3 H D), x2 -> W2 -> y2}, then the decode step
+    (qkv, caches with `cached` rows + 1, o)"""
+
+    def __init__(self, dev, wdt, T, H, D, K, N2, K2, seed):
+        rng = np.random.default_rng(seed)
+        self.T, self.H, self.D, self.K = T, H, D, K
+        HD = H * D
+        self.Wqkv = dev.random_weight(wdt, 3 * HD, K, seed ^ 0x61, 0.05)
+        self.W2 = dev.random_weight(wdt, N2, K2, seed ^ 0x62, 0.02)
+        self.x = dev.fill_normal(dev.alloc(K * 4), F32, K, seed ^ 0x63, 1.0)
+        self.x2 = dev.fill_normal(dev.alloc(K2 * 4), F32, K2, seed ^ 0x64, 1.0)
+        self.qkv = dev.alloc(3 * HD * 4)
+        self.y2 = dev.alloc(N2 * 4)
+        self.k0 = f16_bits(rng.standard_normal((T + 1, H, D)))
+        self.v0 = f16_bits(rng.standard_normal((T + 1, H, D)))
+        self.kc, self.vc = dev.upload(self.k0), dev.upload(self.v0)
+        self.o = dev.alloc(HD * 4)
+        self.N2, self.K2 = N2, K2
+        self.scratch = dev.alloc(max(3 * HD * K, N2 * K2) * 4)
+
+    def plan(self, dev, fuse=True):
+        p = m.Plan(dev)
+        p.set_fusion(fuse)
+        p.add_gemv_grouped([(self.x, F32, self.Wqkv, self.qkv, F32), (self.x2, F32, self.W2, self.y2, F32)])
+        p.add_attention_decode_step(self.qkv, self.kc, self.vc, self.o, self.T, self.H, self.D)
+        return p
+
+    def reset_caches(self):
+        self.kc.upload(self.k0)
+        self.vc.upload(self.v0)
+
+    def check(self, orc, o, qkv):
+        H, D, T = self.H, self.D, self.T
+        HD = H * D
+        q = f16_bits(qkv[:HD].reshape(1, H, D))
+        kn, vn = f16_bits(qkv[HD:2 * HD].reshape(H, D)), f16_bits(qkv[2 * HD:].reshape(H, D))
+        kc = self.kc.download(np.uint16, (T + 1) * HD).reshape(T + 1, H, D)
+        vc = self.vc.download(np.uint16, (T + 1) * HD).reshape(T + 1, H, D)
+        assert np.array_equal(kc[T], kn) and np.array_equal(vc[T], vn)          # the append, RNE fp16
+        assert np.array_equal(kc[:T], self.k0[:T]) and np.array_equal(vc[:T], self.v0[:T])
+        O64, A, R = orc.attention_f64(q, kc, vc, 1, T + 1, H, D, False, 1.0 / np.sqrt(D))
+        got = o.astype(np.float64).reshape(1, H, D)
+        tol = attention_tol(O64, A, R, T + 1, D)
+        assert np.all(np.isfinite(got))
+        assert np.all(np.abs(got - O64) <= tol), float(np.max(np.abs(got - O64) / tol))
+
+    def free(self):
+        self.Wqkv.free()
+        self.W2.free()
+
+
+@pytest.mark.parametrize("T,H,D", [(0, 32, 64), (1, 32, 64), (100, 32, 64), (512, 32, 64), (2047, 32, 64),
+                                   (300, 16, 128), (33, 5, 64)])
+def test_attention_decode_step_direct(dev, orc, T, H, D):
+    print(f"[decode step] direct T={T} H={H} D={D}", flush=True)
+    rng = np.random.default_rng(T + H)
+    HD = H * D
+    qkv = rng.standard_normal(3 * HD).astype(np.float32)
+    k0 = f16_bits(rng.standard_normal((T + 1, H, D)))
+    v0 = f16_bits(rng.standard_normal((T + 1, H, D)))
+    dq, kc, vc, o = dev.upload(qkv), dev.upload(k0), dev.upload(v0), dev.alloc(HD * 4)
+    dev.attention_decode_step(dq, kc, vc, o, T, H, D)
+    dev.sync()
+    c = StepCase.__new__(StepCase)
+    c.T, c.H, c.D, c.kc, c.vc, c.k0, c.v0 = T, H, D, kc, vc, k0, v0
+    c.check(orc, o.download(np.float32, HD), qkv)
+
+
+@pytest.mark.parametrize("wdt,T,H,D,K", [(m.Q8_0, 512, 32, 64, 2048), (m.Q8_0, 2048, 32, 64, 2048),
+                                         (m.Q4_0, 512, 32, 64, 2048), (m.Q8_0, 0, 32, 64, 2048),
+                                         (m.Q8_0, 300, 16, 128, 1024), (m.F32, 77, 5, 64, 256)])
+def test_fused_decode_step(dev, orc, wdt, T, H, D, K):
+    print(f"[decode step] fused wdt={wdt} T={T} H={H} D={D} K={K}", flush=True)
+    c = StepCase(dev, wdt, T, H, D, K, 3000, 2048, 17)
+    ref = c.plan(dev, fuse=False)
+    assert ref.fused() == 0
+    ref.run(1)
+    ref.check()
+    o_ref, y2_ref = c.o.download(np.float32, H * D), c.y2.download(np.float32, c.N2)
+    qkv_ref = c.qkv.download(np.float32, 3 * H * D)
+    c.check(orc, o_ref, qkv_ref)
+    fused = c.plan(dev, fuse=True)
+    assert fused.fused() == 1
+    fused.use_graph(True)
+    first = None
+    for r in range(4):
+        c.reset_caches()
+        for b in (c.o, c.qkv, c.y2):
+            b.zero()
+        fused.run(1)
+        fused.check()
+        got = (c.o.download(np.float32, H * D), c.qkv.download(np.float32, 3 * H * D),
+               c.y2.download(np.float32, c.N2))
+        if first is None:
+            first = got
+            assert np.array_equal(got[1], qkv_ref) and np.array_equal(got[2], y2_ref)
+            c.check(orc, got[0], got[1])
+            rows = np.unique(np.linspace(0, 3 * H * D - 1, 128).astype(np.int64))
+            gemv_check(orc, c.x.download(np.float32, K), c.Wqkv, got[1], rows, c.scratch)
+        else:
+            for a, b in zip(first, got):
+                assert np.array_equal(a, b), r
+    fused.destroy()
+    ref.destroy()
+    c.free()
+
+
+def test_decode_step_not_fused_when_it_does_not_fit(dev):
+    c = StepCase(dev, m.Q8_0, 64, 32, 64, 2048, 512, 2048, 5)
+    # the other entry reads the cache: not fused
+    p = m.Plan(dev)
+    p.add_gemv_grouped([(c.x, F32, c.Wqkv, c.qkv, F32), (c.kc, F32, c.W2, c.y2, F32)])
+    p.add_attention_decode_step(c.qkv, c.kc, c.vc, c.o, c.T, c.H, c.D)
+    assert p.fused() == 0
+    p.destroy()
+    # no entry writes qkv
+    p = m.Plan(dev)
+    p.add_gemv_grouped([(c.x2, F32, c.W2, c.y2, F32)])
+    p.add_attention_decode_step(c.qkv, c.kc, c.vc, c.o, c.T, c.H, c.D)
+    assert p.fused() == 0
+    p.destroy()
+    # an entry writes o
+    p = m.Plan(dev)
+    p.add_gemv_grouped([(c.x, F32, c.Wqkv, c.qkv, F32), (c.x2, F32, c.W2, c.o, F32)])
+    p.add_attention_decode_step(c.qkv, c.kc, c.vc, c.o, c.T, c.H, c.D)
+    assert p.fused() == 0
+    p.destroy()
+    c.free()
+
+
+def test_decode_step_carried_by_the_readers_launch(dev, orc):
+    """group A writes qkv, the step, group B reads o: the step runs in B's launch
+    (A's launch stays plain), every replay equal, o and B's reader against the
+    oracle"""
+    c = StepCase(dev, m.Q8_0, 512, 32, 64, 2048, 2048, 8192, 23)
+    W3 = dev.random_weight(m.Q8_0, 2048, 2048, 0x91, 0.02)
+    y3 = dev.alloc(2048 * 4)
+
+    def plan(fuse):
+        p = m.Plan(dev)
+        p.set_fusion(fuse)
+        p.add_gemv_grouped([(c.x, F32, c.Wqkv, c.qkv, F32), (c.x2, F32, c.W2, c.y2, F32)])
+        p.add_attention_decode_step(c.qkv, c.kc, c.vc, c.o, c.T, c.H, c.D)
+        p.add_gemv_grouped([(c.o, F32, W3, y3, F32), (c.x2, F32, c.W2, c.y2, F32)])
+        return p
+
+    ref = plan(False)
+    ref.run(1)
+    ref.check()
+    y3_ref = y3.download(np.float32, 2048)
+    p = plan(True)
+    assert p.fused() == 1
+    ms = p.profile()
+    assert ms[0] > 0 and ms[1] == 0 and ms[2] > 0       # the step is timed with B's launch
+    p.use_graph(True)
+    first = None
+    for r in range(4):
+        c.reset_caches()
+        for b in (c.o, c.qkv, y3):
+            b.zero()
+        p.run(1)
+        p.check()
+        got = (c.o.download(np.float32, 2048), c.qkv.download(np.float32, 6144), y3.download(np.float32, 2048))
+        if first is None:
+            first = got
+            c.check(orc, got[0], got[1])
+            rows = np.unique(np.linspace(0, 2047, 128).astype(np.int64))
+            gemv_check(orc, got[0], W3, got[2], rows, c.scratch)
+            assert np.allclose(got[2], y3_ref, rtol=1e-4, atol=1e-4)
+        else:
+            for a, b in zip(first, got):
+                assert np.array_equal(a, b), r
+    p.destroy()
+    ref.destroy()
+    W3.free()
+    c.free()
