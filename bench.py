@@ -242,8 +242,9 @@ def decode_token(dev, m, qt, cache, steps, warmup, fuse=True):
     nbytes = (sum(gemv_bytes(qt, N, K, 1) for _, N, K in PHI_STEP)   # weights, x, y
               + 24 * 2 * (cache + 1) * 32 * 64 * 2.0                  # each layer's KV cache, fp16 (+ the append)
               + 51200 * 4.0)                                          # logits read by the token pick
+    kernels = 24 * 2 + 2 + (0 if fused else 24 * (2 if cache > 128 else 1))   # an unfused step: split + merge
     return {"workload": f"phi15_decode_token_{qt}_cache{cache}" + ("" if fuse else "_unfused"), "us": ms * 1e3,
-            "tokens_per_s": 1e3 / ms, "ops": 24 * 3 + 2, "launches": 24 * 3 + 2 - fused,
+            "tokens_per_s": 1e3 / ms, "ops": 24 * 3 + 2, "kernels": kernels,
             "attention": ("each layer's attention step (cache append + attention over cache + 1 keys) computed "
                           "inside the {QKV, fc1} launch that writes its q, k, v (plan fusion)" if fused
                           else "one attention step launch per layer (split kernel + merge kernel)"),
@@ -252,6 +253,14 @@ def decode_token(dev, m, qt, cache, steps, warmup, fuse=True):
             "bytes_per_token": nbytes,
             "roofline": roofline("hbm", nbytes / ms / 1e6, "timed region (HIP events around the graph replays) "
                                  "/ tokens; bytes = weights, x and y of the 97 GEMVs, the KV cache, the logits")}
+
+
+def token_extras(dev, m, steps, warmup, extra):
+    for qt, cache, fuse in (("q8_0", 512, True), ("q8_0", 512, False), ("q8_0", 2048, True), ("q4_0", 512, True)):
+        r = decode_token(dev, m, qt, cache, steps, warmup, fuse)
+        extra[r["workload"]] = r
+        log(f"[bench]   {r['workload']}: {r['us']:.1f} us/token ({r['tokens_per_s']:.0f} tokens/s; GEMVs, "
+            f"attention, LM head and token pick, one graph of {r['kernels']} kernel launches)")
 
 
 def fp32_gemv(dev, m, steps, warmup, copies=16):
@@ -789,6 +798,8 @@ def main():
     ap.add_argument("--kernel-filter", default="", help="with --counter-table: kernels whose name contains this")
     ap.add_argument("--attention-only", action="store_true",
                     help="only the attention and token-pick workloads (one JSON line of them)")
+    ap.add_argument("--token-only", action="store_true",
+                    help="only the decode-token plans (Q8_0 cache 512 fused and not, 2048; Q4_0 512; one JSON line)")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the prefill / vision GEMM shapes and the batched QK^T (one JSON line of them)")
     ap.add_argument("--gemm-bench", action="store_true",
@@ -846,8 +857,10 @@ def main():
         print(json.dumps({"gemm_bench_matrix": gemm_bench_matrix(dev, m)}), flush=True)
         dev.close()
         return
-    if args.attention_only or args.gemm_only:
+    if args.attention_only or args.gemm_only or args.token_only:
         extra = {}
+        if args.token_only:
+            token_extras(dev, m, max(10, args.steps // 2), 3, extra)
         if args.gemm_only:
             gemm_extras(dev, m, 20, 5, extra)
         if args.attention_only:
@@ -869,12 +882,7 @@ def main():
             extra[r["workload"]] = r
             log(f"[bench]   {r['workload']}: {r['ms_per_step'] * 1e3:.1f} us/step {r['gbs']:.0f} GB/s "
                 f"({100 * r['frac']:.1f}%)")
-        for qt, cache, fuse in (("q8_0", 512, True), ("q8_0", 512, False), ("q8_0", 2048, True),
-                                ("q4_0", 512, True)):
-            r = decode_token(dev, m, qt, cache, max(10, args.steps // 2), 3, fuse)
-            extra[r["workload"]] = r
-            log(f"[bench]   {r['workload']}: {r['us']:.1f} us/token ({r['tokens_per_s']:.0f} tokens/s; GEMVs, "
-                f"attention, LM head and token pick, one graph of {r['launches']} launches)")
+        token_extras(dev, m, max(10, args.steps // 2), 3, extra)
         r = fp32_gemv(dev, m, max(10, args.steps // 2), 3)
         extra[r["workload"]] = r
         log(f"[bench]   {r['workload']}: {r['us']:.1f} us {r['gbs']:.0f} GB/s ({100 * r['frac']:.1f}%)")

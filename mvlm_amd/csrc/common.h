@@ -235,12 +235,12 @@ struct StreamAttnDesc {
     float* o = nullptr;
     int heads = 0, head_dim = 0, cached = 0, mode = 0, step = 0;
     float scale = 0.0f;
-    void* workspace = nullptr;     // stream_attn_workspace_bytes(heads, head_dim, keys attended, CUs)
+    void* workspace = nullptr;     // stream_attn_workspace_bytes(heads, head_dim, cached, step, CUs)
     void* sync = nullptr;          // SYNC_BYTES of the launch site, zeroed before its first launch
 };
 constexpr size_t SYNC_BYTES = 64 * 1024;
 constexpr size_t SYNC_ERR_OFFSET = 256;   // u32 error word of a sync area
-size_t stream_attn_workspace_bytes(int heads, int head_dim, int seq_kv, int num_cus);
+size_t stream_attn_workspace_bytes(int heads, int head_dim, int cached, int step, int num_cus);
 // hipSuccess when this launch can carry the attention: M = 1, head_dim 64 or
 // 128, mode 0 with fp32 x and rows of at most 4 KiB for the waiting problems,
 // mode 1 with one fp32 problem output equal to qkv, and the workgroups that

@@ -256,53 +256,22 @@ __device__ __forceinline__ void attn_producer_done(const StreamAttn& a, int j, i
 // holds key `cached` takes the new key from qkv (wave 0) and writes it and
 // the new value to the caches.  flag_ok: one word of LDS for the wait.
 template <int D>
-__device__ void attn_decode_block(const StreamAttn& a, int b, float* lds, uint32_t* flag_ok, int wave, int lane) {
+__device__ __forceinline__ void attn_decode_block(const StreamAttn& a, int b, float* lds, uint32_t* flag_ok, int wave,
+                                                  int lane) {
     constexpr int LPK = D / 8;                 // lanes per key
     constexpr int KPI = 64 / LPK;              // keys per wave-wide load
     constexpr int KPW = ATTN_NL * KPI;         // keys per wave and iteration
     constexpr int DPL = D / 64;                // output dims per lane in the merges
     const int h = b / a.splits, sp = b - h * a.splits;
-    const int k0 = sp * a.keys_per_split, k1 = min(k0 + a.keys_per_split, a.seq_kv);
-    const int kc1 = min(k1, a.cached);         // this split's keys in the cache: [k0, kc1)
+    // a step's last split holds only the new key (index `cached`); the others
+    // cut the cached keys
+    const bool new_key = a.step && sp == a.splits - 1;
+    const int k0 = sp * a.keys_per_split, kc1 = new_key ? k0 : min(k0 + a.keys_per_split, a.cached);
     const int sub = lane % LPK, kl = lane / LPK;
     const int64_t key_stride = (int64_t)a.heads * D;
     const int col = h * D + sub * 8;
-    // the first iteration's keys and values (they do not depend on the producers)
-    u32x4 kr[ATTN_NL], vr[ATTN_NL];
-    int base = k0 + wave * KPW;
-    auto load_kv = [&](int at) {
-#pragma unroll
-        for (int j = 0; j < ATTN_NL; ++j) {
-            const int64_t r = min(at + j * KPI + kl, kc1 - 1);
-            kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.k + r * key_stride + col));
-        }
-#pragma unroll
-        for (int j = 0; j < ATTN_NL; ++j) {
-            const int64_t r = min(at + j * KPI + kl, kc1 - 1);
-            vr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.v + r * key_stride + col));
-        }
-    };
-    if (base < kc1) load_kv(base);
     bool ok = true;
     float qf[8];
-    if (a.step) {
-        if (a.mode == 1 && a.prod_blocks > 0) ok = attn_wait_producers(a, b, h, wave, lane, flag_ok);
-        const __amdgpu_buffer_rsrc_t qr = dev_rsrc(a.qkv, 3 * a.heads * D * 4);
-        const u32x4 u0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, col * 4, 0, kCpolDevice));
-        const u32x4 u1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, col * 4 + 16, 0, kCpolDevice));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            qf[e] = f16_round(__uint_as_float(u0[e])) * a.scale_log2;
-            qf[4 + e] = f16_round(__uint_as_float(u1[e])) * a.scale_log2;
-        }
-    } else {
-        const u32x4 u = *reinterpret_cast<const u32x4*>(a.q + col);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            qf[2 * j] = f16_bits_to_f32((uint16_t)(u[j] & 0xFFFFu)) * a.scale_log2;
-            qf[2 * j + 1] = f16_bits_to_f32((uint16_t)(u[j] >> 16)) * a.scale_log2;
-        }
-    }
     float m = -INFINITY, l = 0.0f, o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = 0.0f;
@@ -343,36 +312,80 @@ __device__ void attn_decode_block(const StreamAttn& a, int b, float* lds, uint32
         }
         m = mn;
     };
-    for (; base < kc1; base += NWAVE * KPW) {
-        bool valid[ATTN_NL];
+    // q, rounded to fp16, in the exp2 domain: from qkv (a step, after its
+    // producers in mode 1) or the fp16 q
+    auto load_q = [&]() {
+        if (a.step) {
+            if (a.mode == 1 && a.prod_blocks > 0) ok = attn_wait_producers(a, b, h, wave, lane, flag_ok);
+            const __amdgpu_buffer_rsrc_t qr = dev_rsrc(a.qkv, 3 * a.heads * D * 4);
+            const u32x4 u0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, col * 4, 0, kCpolDevice));
+            const u32x4 u1 =
+                __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, col * 4 + 16, 0, kCpolDevice));
 #pragma unroll
-        for (int j = 0; j < ATTN_NL; ++j) valid[j] = base + j * KPI + kl < kc1;
-        process(kr, vr, valid, std::integral_constant<int, ATTN_NL>{});
-        if (base + NWAVE * KPW < kc1) load_kv(base + NWAVE * KPW);
-    }
-    if (a.step && k1 == a.seq_kv && wave == 0) {   // the new key, index `cached`
-        const __amdgpu_buffer_rsrc_t qr = dev_rsrc(a.qkv, 3 * a.heads * D * 4);
-        u32x4 kb[1], vb[1];
+            for (int e = 0; e < 4; ++e) {
+                qf[e] = f16_round(__uint_as_float(u0[e])) * a.scale_log2;
+                qf[4 + e] = f16_round(__uint_as_float(u1[e])) * a.scale_log2;
+            }
+        } else {
+            const u32x4 u = *reinterpret_cast<const u32x4*>(a.q + col);
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int off = col * 4 + 16 * half;
-            const u32x4 kf = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                           qr, a.heads * D * 4 + off, 0, kCpolDevice));
-            const u32x4 vf = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                           qr, 2 * a.heads * D * 4 + off, 0, kCpolDevice));
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                kb[0][2 * half + e] = (uint32_t)f32_to_f16_bits(__uint_as_float(kf[2 * e])) |
-                                      ((uint32_t)f32_to_f16_bits(__uint_as_float(kf[2 * e + 1])) << 16);
-                vb[0][2 * half + e] = (uint32_t)f32_to_f16_bits(__uint_as_float(vf[2 * e])) |
-                                      ((uint32_t)f32_to_f16_bits(__uint_as_float(vf[2 * e + 1])) << 16);
+            for (int j = 0; j < 4; ++j) {
+                qf[2 * j] = f16_bits_to_f32((uint16_t)(u[j] & 0xFFFFu)) * a.scale_log2;
+                qf[2 * j + 1] = f16_bits_to_f32((uint16_t)(u[j] >> 16)) * a.scale_log2;
             }
         }
-        const bool valid[1] = {kl == 0};
-        process(kb, vb, valid, std::integral_constant<int, 1>{});
-        if (kl == 0) {   // the cache append: row `cached` of head h, this lane's 8 dims
-            *reinterpret_cast<u32x4*>(a.k + (int64_t)a.cached * key_stride + col) = kb[0];
-            *reinterpret_cast<u32x4*>(a.v + (int64_t)a.cached * key_stride + col) = vb[0];
+    };
+    // the first iteration's cached keys and values, requested before q (they
+    // do not depend on the producers)
+    u32x4 kr[ATTN_NL], vr[ATTN_NL];
+    int base = k0 + wave * KPW;
+    auto load_kv = [&](int at) {
+#pragma unroll
+        for (int j = 0; j < ATTN_NL; ++j) {
+            const int64_t r = min(at + j * KPI + kl, kc1 - 1);
+            kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.k + r * key_stride + col));
+        }
+#pragma unroll
+        for (int j = 0; j < ATTN_NL; ++j) {
+            const int64_t r = min(at + j * KPI + kl, kc1 - 1);
+            vr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.v + r * key_stride + col));
+        }
+    };
+    if (base < kc1) load_kv(base);
+    load_q();
+    if (new_key) {
+        if (wave == 0) {   // the new key and value, rounded to fp16: attended and appended to the caches
+            const __amdgpu_buffer_rsrc_t qr = dev_rsrc(a.qkv, 3 * a.heads * D * 4);
+            u32x4 kb[1], vb[1];
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const int off = col * 4 + 16 * half;
+                const u32x4 kf = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                               qr, a.heads * D * 4 + off, 0, kCpolDevice));
+                const u32x4 vf = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                               qr, 2 * a.heads * D * 4 + off, 0, kCpolDevice));
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    kb[0][2 * half + e] = (uint32_t)f32_to_f16_bits(__uint_as_float(kf[2 * e])) |
+                                          ((uint32_t)f32_to_f16_bits(__uint_as_float(kf[2 * e + 1])) << 16);
+                    vb[0][2 * half + e] = (uint32_t)f32_to_f16_bits(__uint_as_float(vf[2 * e])) |
+                                          ((uint32_t)f32_to_f16_bits(__uint_as_float(vf[2 * e + 1])) << 16);
+                }
+            }
+            const bool valid[1] = {kl == 0};
+            process(kb, vb, valid, std::integral_constant<int, 1>{});
+            if (kl == 0) {   // row `cached` of head h, this lane's 8 dims
+                *reinterpret_cast<u32x4*>(a.k + (int64_t)a.cached * key_stride + col) = kb[0];
+                *reinterpret_cast<u32x4*>(a.v + (int64_t)a.cached * key_stride + col) = vb[0];
+            }
+        }
+    } else {
+        for (; base < kc1; base += NWAVE * KPW) {
+            bool valid[ATTN_NL];
+#pragma unroll
+            for (int j = 0; j < ATTN_NL; ++j) valid[j] = base + j * KPI + kl < kc1;
+            process(kr, vr, valid, std::integral_constant<int, ATTN_NL>{});
+            if (base + NWAVE * KPW < kc1) load_kv(base + NWAVE * KPW);
         }
     }
     // sums over the wave's key groups: lanes of one sub end with the wave's totals
@@ -979,10 +992,20 @@ static void attn_split(int heads, int D, int seq_kv, int num_cus, int* splits, i
 
 static int attn_seq(const StreamAttnDesc& d) { return d.cached + (d.step ? 1 : 0); }
 
-size_t stream_attn_workspace_bytes(int heads, int head_dim, int seq_kv, int num_cus) {
-    if (heads < 1 || (head_dim != 64 && head_dim != 128) || seq_kv < 1) return 0;
+// Splits of the cached keys (none for a step over an empty cache), plus a
+// step's split for the new key.  Every split of cached keys holds at least
+// one key.
+static void attn_layout(int heads, int head_dim, int cached, int step, int num_cus, int* splits, int* kps) {
+    *splits = 0;
+    *kps = 1;
+    if (cached > 0) attn_split(heads, head_dim, cached, num_cus, splits, kps);
+    *splits += step ? 1 : 0;
+}
+
+size_t stream_attn_workspace_bytes(int heads, int head_dim, int cached, int step, int num_cus) {
+    if (heads < 1 || (head_dim != 64 && head_dim != 128) || cached < 0 || cached + step < 1) return 0;
     int splits = 1, kps = 0;
-    attn_split(heads, head_dim, seq_kv, num_cus > 0 ? num_cus : 256, &splits, &kps);
+    attn_layout(heads, head_dim, cached, step, num_cus > 0 ? num_cus : 256, &splits, &kps);
     return ((size_t)heads * splits * head_dim * 4 + 15) / 16 * 16 + (size_t)heads * splits * 8;
 }
 
@@ -1006,7 +1029,7 @@ static bool attn_fill(StreamAttn& a, const StreamAttnDesc& d, int num_cus) {
     a.seq_kv = seq;
     a.mode = d.mode;
     a.step = d.step ? 1 : 0;
-    attn_split(d.heads, d.head_dim, seq, num_cus, &a.splits, &a.keys_per_split);
+    attn_layout(d.heads, d.head_dim, d.cached, d.step, num_cus, &a.splits, &a.keys_per_split);
     a.part_o = (float*)d.workspace;
     a.part_ml = a.part_o + (size_t)d.heads * a.splits * d.head_dim;
     a.blocks = d.heads * a.splits;

@@ -253,7 +253,7 @@ int make_attn_step(mvlm_device* dev, const mvlm_buffer* qkv, mvlm_buffer* Kc, mv
     op->N = cached; op->batch = heads; op->K = head_dim;
     op->scale = scale == 0.0f ? 1.0f / sqrtf((float)head_dim) : scale;
     op->num_cus = dev->prop.multiProcessorCount;
-    op->workspace_bytes = stream_attn_workspace_bytes(heads, head_dim, cached + 1, op->num_cus);
+    op->workspace_bytes = stream_attn_workspace_bytes(heads, head_dim, cached, 1, op->num_cus);
     return device_scratch(dev, op->workspace_bytes, &op->workspace);
 }
 
@@ -729,7 +729,7 @@ static void mark_fusable(mvlm_plan* plan, Op& op) {
     } else {
         d.q = a.a; d.k = const_cast<void*>(a.b); d.v = const_cast<void*>(a.v); d.o = (float*)a.c;
         d.heads = a.batch; d.head_dim = a.K; d.cached = a.N; d.scale = a.scale;
-        if (device_scratch(plan->dev, stream_attn_workspace_bytes(d.heads, d.head_dim, d.cached, op.num_cus),
+        if (device_scratch(plan->dev, stream_attn_workspace_bytes(d.heads, d.head_dim, d.cached, 0, op.num_cus),
                            &d.workspace) != MVLM_OK)
             return;
     }
