@@ -983,7 +983,7 @@ static hipError_t launch_group_x(hipStream_t s, int x_dtype, StreamGroup& g, siz
 static void attn_split(int heads, int D, int seq_kv, int num_cus, int* splits, int* keys_per_split) {
     const int kb = NWAVE * ATTN_NL * (64 / (D / 8));
     int want = std::max(1, (num_cus + heads - 1) / heads);
-    if (const char* e = std::getenv("MVLM_ATTN_SPLITS")) want = std::max(1, std::atoi(e));   // tuning override
+    if (const char* e = std::getenv("MVLM_DECODE_SPLITS")) want = std::max(1, std::atoi(e));   // tuning override
     const int s = std::max(1, std::min(std::min((seq_kv + kb - 1) / kb, want), ATTN_MAX_SPLITS));
     const int k = ((seq_kv + s - 1) / s + kb - 1) / kb * kb;
     *keys_per_split = k;
