@@ -605,7 +605,7 @@ def pmc_probe(steps=3):
 
 
 PMC_WORKLOADS = ("decode_q8_0_m1", "decode_q4_0_m1", "decode_q4_0_m4", "decode_q4_0_m16", "decode_q8_0_m4", "gemm",
-                 "gemm_bf16", "gemv_f32", "gemv_exact", "qk_batched", "attention", "argmax")
+                 "gemm_bf16", "gemv_f32", "gemv_exact", "qk_batched", "attention", "argmax", "token")
 
 
 def pmc_workload(name, reps=2):
@@ -671,6 +671,10 @@ def pmc_workload(name, reps=2):
             plan = m.Plan(dev)
             plan.add_attention(Q, K, V, O, m.F16, sq, skv, H, D, causal=causal)
             plans.append((aname, plan))
+    elif name == "token":   # the Q8_0 token plan at cache 512, attention fused into the launches
+        plan, ws, _ = build_token_plan(dev, m, "q8_0", 512, True)
+        plans.append((name, plan))
+        weights += ws
     elif name == "argmax":
         n = PHI_LM_HEAD[1]
         x = dev.fill_normal(dev.alloc(n * 4), m.F32, n, SEED ^ 0x601, 1.0)
