@@ -15,7 +15,7 @@
 // aligned LDS chunks; at most 3 + 3 floats at the ends use 4-byte stores).
 //
 // A workgroup serves one batch and the row blocks p, p + P, p + 2P, ...  Its
-// 8 waves split the columns (16-column blocks dealt in turn, at most 8 per
+// 16 waves split the columns (16-column blocks dealt in turn, at most 4 per
 // wave) and load the B fragments of their columns into registers once, for
 // every row block they compute: B (K of attention) is read from L2 once per
 // workgroup instead of once per row block.  The A rows of all its row blocks
@@ -24,15 +24,36 @@
 // flight while the next blocks are computed (loads and stores share that
 // counter, so a wait for a load would also wait for them).
 //
-// Products: v_mfma_f32_16x16x32_{f16,bf16}.  Operand layout: lane l supplies
-// A[l%16][8*(l/16) .. +7] and B^T[l%16][8*(l/16) .. +7] for k-step ks (K
-// offset 32 ks); accumulator register i of lane l is C[4*(l/16) + i][l%16].
+// Schedule.  Per-phase s_memrealtime stamps of an instrumented copy (SigLIP
+// scores, 16 workgroups per batch) showed the earlier 8-wave form spending
+// ~3.7 us before its first product, then ~1.2 us of products and ~0.8 us of
+// store issue per row block, one after another.  Now: 16 waves share the
+// columns (half the products per wave); the A loads are issued before B's and
+// written to LDS while B's are in flight, and the first block's products wait
+// for their own B fragments only (loads return in order); a block's
+// accumulator chains are issued together before any is written to LDS; the
+// staging area is double-buffered, so one barrier per block separates the
+// products of block i + 1 from the stores of block i; the store phase issues
+// all its LDS reads before its stores; and the stores write through the XCD's
+// L2 (sc1), so the 34 MB of scores do not sit in L2 as dirty lines that the
+// end of the kernel has to write back.  Measured on the SigLIP shape, 16
+// copies in one graph: 13.2 us (8 waves) -> 11.8 (write-through stores) ->
+// 10.6 us.  The row blocks then follow each other ~1.6 us apart, which is the
+// time HBM takes to absorb one round of them (12 MB over the 256 workgroups):
+// what is left above the write time is the ~4 us before the first stores.
+//
+// Products: v_mfma_f32_16x16x32_{f16,bf16} with B's fragment as the first
+// operand, so the accumulator holds the block transposed.  Operand layout:
+// lane l supplies B^T[l%16][8*(l/16) .. +7] and A[l%16][8*(l/16) .. +7] for
+// k-step ks (K offset 32 ks); accumulator register i of lane l is
+// C[l%16][4*(l/16) + i]: four consecutive columns of one row, written to LDS
+// as two 8-byte pairs (the 16 rows of a block are N floats apart, 25 banks
+// for N = 729, so a quarter-wave's pairs fall in distinct banks).
 // K is a multiple of 8: an 8-element group is inside K or past it, and groups
-// past K are zero in registers (never loaded: B's groups past K may lie past
-// its buffer).  Rows of A past M load row M - 1 and columns of B past N load
-// column N - 1; their products are never stored.  fp16/bf16 products are exact
-// in fp32; the matrix core's accumulation order differs from an fma chain in
-// ascending k, within the 1e-3 relative bound of 16-bit inputs.
+// past K are zero in registers (their buffer loads are out of range).  Rows of A past M load row M - 1 and columns of B past N
+// load column N - 1; their products are never stored.  fp16/bf16 products are
+// exact in fp32; the matrix core's accumulation order differs from an fma
+// chain in ascending k, within the 1e-3 relative bound of 16-bit inputs.
 #include "common.h"
 #include "device_math.h"
 
@@ -50,10 +71,12 @@ struct SmallKArgs {
     int per_batch;             // workgroups per batch (P)
 };
 
-constexpr int SK_WAVES = 8;
+constexpr int SK_WAVES = 16;
 constexpr int SK_ROWS = 16;
 constexpr int SK_LDS_MAX = 160 * 1024;
-constexpr int SK_MAXB = 8;     // 16-column blocks per wave: N <= 16 * 8 * 8 = 1024 (6 when N <= 768)
+constexpr int SK_MAXB = 4;     // 16-column blocks per wave: N <= 16 * 16 * 4 = 1024 (3 when N <= 768)
+constexpr int SK_A_EARLY = 1;  // A groups per thread loaded before B's loads
+constexpr int SK_CPOL_WT = 16; // sc1: the store writes through the XCD's L2
 
 typedef _Float16 skf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 skbf16x8 __attribute__((ext_vector_type(8)));
@@ -77,101 +100,169 @@ __device__ __forceinline__ void sk_lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// 16 bytes at p if the 8-element group starting at k lies inside K, else zeros
-__device__ __forceinline__ u32x4 sk_load(const uint16_t* p, int k, int K) {
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (k < K) v = *reinterpret_cast<const u32x4*>(p);
-    return v;
+// The 8-element group starting at element k of the row at element offset
+// `row` of an operand (raw buffer `r`): a group past K reads at an offset
+// beyond the buffer's size, which returns zeros and moves no data.  No branch
+// around the load, so the compiler counts the loads in flight exactly and
+// waits for each one alone.  (Reading the row's last group inside K instead
+// made the load phase ~0.7 us longer: the first loads' time is set by the
+// bytes the CUs take in.)
+constexpr int SK_OOB = 0x7FFFFFF0;   // beyond every operand (sizes are checked below 2^30 bytes)
+__device__ __forceinline__ u32x4 sk_load(__amdgpu_buffer_rsrc_t r, int row, int k, int K) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, k < K ? 2 * (row + k) : SK_OOB, 0, 0));
 }
 
 template <bool BF16, int KS, int MAXB>
 __global__ __launch_bounds__(64 * SK_WAVES) void gemm_smallk_kernel(const SmallKArgs p) {
-    extern __shared__ __attribute__((aligned(16))) float stage[];   // 16 N + 3 floats
+    // LDS: two staging areas of SA floats (16 N + 3 each, rounded up to 16
+    // bytes), the A rows of the workgroup's row blocks, a spare 16-byte slot
+    extern __shared__ __attribute__((aligned(16))) float smem[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int b = blockIdx.x / p.per_batch, first = blockIdx.x % p.per_batch;
-    const int N = p.N, K = p.K;
-    const uint16_t* __restrict__ A = p.A + (int64_t)b * p.sA;
-    const uint16_t* __restrict__ B = p.B + (int64_t)b * p.sB;
+    // workgroup x runs on XCD x % 8: the workgroups of one batch are numbered
+    // so that they share an XCD (and its L2 copy of B) when the grid allows
+    int w = blockIdx.x;
+    if ((gridDim.x & 7) == 0) w = (w & 7) * (gridDim.x >> 3) + (w >> 3);
+    const int b = w / p.per_batch, first = w % p.per_batch;
+    const int N = p.N, K = p.K, M = p.M;
+    const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(p.A + (int64_t)b * p.sA), 0, (int)(2 * ((int64_t)(M - 1) * p.lda + K)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(p.B + (int64_t)b * p.sB), 0, (int)(2 * ((int64_t)(N - 1) * p.ldb + K)), 0x00020000);
     const int kq = 8 * (lane >> 4);          // this lane's 8-element group within a k-step
     const int nb = (N + 15) / 16;            // 16-column blocks, dealt to the waves in turn
     const int mine = (nb - wave + SK_WAVES - 1) / SK_WAVES;
+    const int nblk = (p.row_blocks - first + p.per_batch - 1) / p.per_batch;
+    if (nblk <= 0) return;
+    const int SA = (SK_ROWS * N + 3 + 3) & ~3;
+    uint16_t* arows = reinterpret_cast<uint16_t*>(smem + 2 * SA);
+    constexpr int RE = KS * 32;              // elements per staged A row
+    constexpr int GPR = RE / 8;              // 8-element groups per staged A row
+    const int agroups = nblk * SK_ROWS * GPR;
+    auto a_row = [&](int c) {                // element offset of the A row of staged group c
+        const int r = c / GPR;
+        return min((first + p.per_batch * (r / SK_ROWS)) * SK_ROWS + r % SK_ROWS, M - 1) * (int)p.lda;
+    };
 
-    // this wave's B fragments, for every row block of the workgroup
+    // 1. the first A groups of this thread, then every B fragment of this wave
+    //    (columns of blocks past `mine` load column N - 1 and are never stored)
+    //    (a wave with no A group left loads nothing: an out-of-range load took
+    //    ~2.4 us to return zeros here, a load from memory ~0.4 us)
+    u32x4 ae[SK_A_EARLY];
+#pragma unroll
+    for (int u = 0; u < SK_A_EARLY; ++u) {
+        const int c = (int)threadIdx.x + 64 * SK_WAVES * u;
+        if (64 * (wave + SK_WAVES * u) < agroups) ae[u] = sk_load(ar, a_row(min(c, agroups - 1)), (min(c, agroups - 1) % GPR) * 8, K);
+    }
     u32x4 bf[MAXB][KS];
 #pragma unroll
     for (int j = 0; j < MAXB; ++j) {
         const int col = min((wave + SK_WAVES * j) * 16 + (lane & 15), N - 1);
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            bf[j][ks] = (u32x4){0u, 0u, 0u, 0u};
-            if (j < mine) bf[j][ks] = sk_load(B + (int64_t)col * p.ldb + 32 * ks + kq, 32 * ks + kq, K);
-        }
+        for (int ks = 0; ks < KS; ++ks) bf[j][ks] = sk_load(br, col * (int)p.ldb, 32 * ks + kq, K);
     }
-    // the A rows of all this workgroup's row blocks into LDS, zero past K
-    // (area: blocks x 16 rows x KS x 32 elements, after the staging area)
-    const int nblk = (p.row_blocks - first + p.per_batch - 1) / p.per_batch;
-    uint16_t* arows = reinterpret_cast<uint16_t*>(stage + ((SK_ROWS * N + 3 + 3) & ~3));
-    constexpr int RE = KS * 32;   // elements per staged row
-    for (int c = threadIdx.x; c < nblk * SK_ROWS * (RE / 8); c += 64 * SK_WAVES) {
-        const int r = c / (RE / 8), k = (c % (RE / 8)) * 8;
-        const int row = min((first + p.per_batch * (r / SK_ROWS)) * SK_ROWS + r % SK_ROWS, p.M - 1);
-        *reinterpret_cast<u32x4*>(arows + r * RE + k) = sk_load(A + (int64_t)row * p.lda + k, k, K);
+    // 2. A into LDS (zero past K); groups beyond the early ones (many row blocks
+    //    per workgroup) are loaded here, after B's loads
+    // (a group past the last goes to a spare slot after the A rows: the write
+    // has no branch, so the compiler cannot sink its load below B's)
+#pragma unroll
+    for (int u = 0; u < SK_A_EARLY; ++u) {
+        const int c = (int)threadIdx.x + 64 * SK_WAVES * u;
+        const int slot = c < agroups ? (c / GPR) * RE + (c % GPR) * 8 : agroups * 8;
+        if (64 * (wave + SK_WAVES * u) < agroups) *reinterpret_cast<u32x4*>(arows + slot) = ae[u];
     }
-    // every B fragment lands before the loop and is redefined by a pin: inside
-    // the loop no instruction waits on a load the compiler tracks (such a wait
-    // would be a vmcnt(0), which also waits for the stores in flight)
-#pragma unroll
-    for (int j = 0; j < MAXB; ++j)
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) asm_pin(bf[j][ks]);
-    __syncthreads();
+    for (int c = (int)threadIdx.x + 64 * SK_WAVES * SK_A_EARLY; c < agroups; c += 64 * SK_WAVES)
+        *reinterpret_cast<u32x4*>(arows + (c / GPR) * RE + (c % GPR) * 8) = sk_load(ar, a_row(c), (c % GPR) * 8, K);
+    sk_lds_barrier();
 
-    for (int i = 0; i < nblk; ++i) {
-        const int rb = first + p.per_batch * i;
-        const int i0 = rb * SK_ROWS, rows = min(SK_ROWS, p.M - i0);
-        const int64_t g0 = (int64_t)b * p.sC + (int64_t)i0 * N;   // first float of this block's range
-        const int s = (int)(g0 & 3);                              // LDS index of element t is t + s
+    // products of row block i into staging area buf (LDS index of the block's
+    // element t is t + its shift)
+    auto compute = [&](int i, float* stage) {
+        const int i0 = (first + p.per_batch * i) * SK_ROWS, rows = min(SK_ROWS, M - i0);
+        const int s = (int)(((int64_t)b * p.sC + (int64_t)i0 * N) & 3);
         u32x4 a[KS];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
             a[ks] = *reinterpret_cast<const u32x4*>(arows + (i * SK_ROWS + (lane & 15)) * RE + 32 * ks + kq);
+        f32x4 acc[MAXB];
 #pragma unroll
         for (int j = 0; j < MAXB; ++j) {
-            if (j < mine) {
-                f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            acc[j] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) acc = sk_mfma<BF16>(a[ks], bf[j][ks], acc);
-                const int col = (wave + SK_WAVES * j) * 16 + (lane & 15);
-                if (col < N) {
+            for (int ks = 0; ks < KS; ++ks) acc[j] = sk_mfma<BF16>(bf[j][ks], a[ks], acc[j]);
+        }
+        // lane l holds row l % 16, columns 4 (l / 16) .. + 3 of each of its blocks
+        const int r = lane & 15;
+        float* row = stage + s + r * N;
 #pragma unroll
-                    for (int i2 = 0; i2 < 4; ++i2) {
-                        const int r = 4 * (lane >> 4) + i2;
-                        if (r < rows) stage[s + r * N + col] = acc[i2];
-                    }
+        for (int j = 0; j < MAXB; ++j) {
+            const int col = (wave + SK_WAVES * j) * 16 + 4 * (lane >> 4);
+            if (j < mine && r < rows) {
+                if (col + 3 < N) {
+#pragma unroll
+                    for (int i2 = 0; i2 < 4; ++i2) row[col + i2] = acc[j][i2];
+                } else {
+#pragma unroll
+                    for (int i2 = 0; i2 < 4; ++i2)
+                        if (col + i2 < N) row[col + i2] = acc[j][i2];
                 }
             }
         }
-        sk_lds_barrier();
-        // the range [g0, g0 + L): e head floats up to the first 16-byte boundary,
-        // whole aligned chunks, then the tail
+    };
+    // the range [g0, g0 + L) of row block i: e head floats up to the first
+    // 16-byte boundary, whole aligned chunks, then the tail
+    auto store = [&](int i, const float* stage) {
+        const int i0 = (first + p.per_batch * i) * SK_ROWS, rows = min(SK_ROWS, M - i0);
+        const int64_t g0 = (int64_t)b * p.sC + (int64_t)i0 * N;
+        const int s = (int)(g0 & 3);
         const int L = rows * N;
         const int e = min((4 - s) & 3, L);
-        float* __restrict__ C = p.C + g0;
+        const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(p.C + g0, 0, L * 4, 0x00020000);
         const int t = threadIdx.x;
-        if (t < e) C[t] = stage[s + t];
         const int chunks = (L - e) >> 2;
-        for (int q = t; q < chunks; q += 64 * SK_WAVES)
-            *reinterpret_cast<f32x4*>(C + e + 4 * q) = *reinterpret_cast<const f32x4*>(stage + s + e + 4 * q);
+        // s + e is 0 or 4 whenever a chunk exists: the chunks' LDS reads are 16-byte aligned
+        const float* src = stage + ((s + e + 3) & ~3);
+        constexpr int U = MAXB;              // chunks per thread: 16 N / 4 / 1024 = N / 256 <= MAXB
+        f32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int q = t + 64 * SK_WAVES * u;
+            if (q < chunks) v[u] = *reinterpret_cast<const f32x4*>(src + 4 * q);
+        }
+        if (t < e) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(stage[s + t]), cr, 4 * t, 0, SK_CPOL_WT);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int q = t + 64 * SK_WAVES * u;
+            if (q < chunks)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[u]), cr, 4 * (e + 4 * q), 0,
+                                                       SK_CPOL_WT);
+        }
         const int tail0 = e + 4 * chunks;
-        if (t < L - tail0) C[tail0 + t] = stage[s + tail0 + t];
-        sk_lds_barrier();   // the staging area is read before the next block overwrites it; the stores drain
+        if (t < L - tail0)
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(stage[s + tail0 + t]), cr, 4 * (tail0 + t), 0,
+                                                  SK_CPOL_WT);
+    };
+
+    compute(0, smem);
+    sk_lds_barrier();
+    // every B fragment has landed (block 0 used them all) and is redefined by a
+    // pin: inside the loop no instruction waits on a load the compiler tracks
+    // (such a wait would be a vmcnt(0), which also waits for the stores in flight)
+#pragma unroll
+    for (int j = 0; j < MAXB; ++j)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) asm_pin(bf[j][ks]);
+    for (int i = 0; i < nblk; ++i) {
+        store(i, smem + (i & 1) * SA);
+        if (i + 1 < nblk) compute(i + 1, smem + ((i + 1) & 1) * SA);
+        sk_lds_barrier();   // block i + 1 staged before its stores; block i's area read before block i + 2 reuses it
     }
 }
 
 bool smallk_supported(int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc, int64_t sA, int64_t sB,
                       const void* A, const void* B, const void* C) {
-    (void)M;
-    return K <= 128 && K % 8 == 0 && ldc == N && N <= 16 * SK_WAVES * SK_MAXB && lda % 8 == 0 && ldb % 8 == 0 &&
+    // operand rows addressed with 32-bit byte offsets, below the out-of-range offset
+    const bool offsets = (int64_t)M * lda * 2 < (1 << 30) && (int64_t)N * ldb * 2 < (1 << 30);
+    return offsets && K <= 128 && K % 8 == 0 && ldc == N && N <= 16 * SK_WAVES * SK_MAXB && lda % 8 == 0 && ldb % 8 == 0 &&
            sA % 8 == 0 && sB % 8 == 0 && ((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 &&
            ((uintptr_t)C & 15) == 0;
 }
@@ -201,11 +292,12 @@ hipError_t launch_gemm_smallk(hipStream_t s, const void* A, int ab_dtype, const 
     }
     p.per_batch = std::max(1, std::min(p.row_blocks, per));
     const int ks = (K + 31) / 32;
-    // LDS: the staging area (16 N + 3 floats, rounded to 16 bytes) and the A
-    // rows of the workgroup's row blocks (16 rows x 32 ks elements each)
+    // LDS: two staging areas (16 N + 3 floats each, rounded to 16 bytes), the A
+    // rows of the workgroup's row blocks (16 rows x 32 ks elements each) and a
+    // spare 16-byte slot
     auto lds_bytes = [&](int per_batch) {
         const int nblk = (p.row_blocks + per_batch - 1) / per_batch;
-        return (uint32_t)(((SK_ROWS * N + 6) & ~3) * 4 + nblk * SK_ROWS * ks * 32 * 2);
+        return (uint32_t)(2 * ((SK_ROWS * N + 6) & ~3) * 4 + nblk * SK_ROWS * ks * 32 * 2 + 16);
     };
     while (lds_bytes(p.per_batch) > SK_LDS_MAX && p.per_batch < p.row_blocks) ++p.per_batch;
     const uint32_t lds = lds_bytes(p.per_batch);
@@ -219,7 +311,7 @@ hipError_t launch_gemm_smallk(hipStream_t s, const void* A, int ab_dtype, const 
     } while (0)
 #define SK_LAUNCH(BFV, KSV)                                      \
     do {                                                         \
-        if (N <= 16 * SK_WAVES * 6) SK_LAUNCH3(BFV, KSV, 6);     \
+        if (N <= 16 * SK_WAVES * 3) SK_LAUNCH3(BFV, KSV, 3);     \
         else SK_LAUNCH3(BFV, KSV, SK_MAXB);                      \
     } while (0)
     switch (ks) {

@@ -3,8 +3,9 @@ a dense fp32 C, which each workgroup writes as one contiguous range of 16 rows
 with 16-byte stores aligned in memory.  Checked on every element against the
 oracle's fp32 fma chain (1e-3 * S, S = sum_k |a_k b_k|), over shapes whose
 ranges start at every alignment modulo 16 bytes, row blocks cut short at M,
-column counts that are not multiples of 16, K from 8 to 128, and with the
-bytes between batches (sC > M N) and after C left untouched."""
+column counts that are not multiples of 16, K from 8 to 128, workgroups with
+more A rows to stage than their threads load ahead of B (48 x 400 x 40 x 128),
+and with the bytes between batches (sC > M N) and after C left untouched."""
 from __future__ import annotations
 
 import numpy as np
@@ -20,7 +21,7 @@ SENTINEL = np.float32(-7.25)
 
 @pytest.mark.parametrize("batch,M,N,K,gap", [(1, 1, 1, 8, 0), (2, 15, 5, 24, 3), (3, 17, 33, 64, 1),
                                              (2, 16, 16, 128, 0), (3, 40, 129, 72, 5), (2, 33, 1023, 120, 2),
-                                             (16, 729, 729, 72, 0)])
+                                             (16, 729, 729, 72, 0), (48, 400, 40, 128, 1)])
 def test_smallk_batched_every_element(dev, orc, batch, M, N, K, gap):
     print(f"[smallk] batch={batch} M={M} N={N} K={K} gap={gap}", flush=True)
     H = batch
