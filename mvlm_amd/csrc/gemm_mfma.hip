@@ -91,7 +91,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 // starts 16-byte aligned)
 __device__ __forceinline__ void store_partial4(float* ws, int64_t i, f32x4 v, int n_left) {
     if (n_left >= 4) {
-        *reinterpret_cast<f32x4*>(ws + i) = v;
+        asm_global_store_b128_wt(ws + i, __builtin_bit_cast(u32x4, v));
         return;
     }
 #pragma unroll
@@ -100,7 +100,8 @@ __device__ __forceinline__ void store_partial4(float* ws, int64_t i, f32x4 v, in
 }
 
 // C row `row_off` (element offset of the row), columns col..col+3: epilogue,
-// output dtype, one 16- or 8-byte store when the row is aligned for it
+// output dtype, one 16- or 8-byte store when the row is aligned for it,
+// written through L2 (C is tens of MB at the prefill shapes)
 __device__ __forceinline__ void store_c4(const GemmArgs& p, int64_t row_off, int col, f32x4 v) {
     const int n_left = p.N - col;
     if (n_left <= 0) return;
@@ -114,7 +115,7 @@ __device__ __forceinline__ void store_c4(const GemmArgs& p, int64_t row_off, int
     const int64_t i = row_off + col;
     if (p.vec_c && n_left >= 4) {
         if (p.c_dtype == 0) {
-            *reinterpret_cast<f32x4*>((float*)p.C + i) = v;
+            asm_global_store_b128_wt((float*)p.C + i, __builtin_bit_cast(u32x4, v));
         } else {
             u32x2 h;
             if (p.c_dtype == 1) {
@@ -124,7 +125,7 @@ __device__ __forceinline__ void store_c4(const GemmArgs& p, int64_t row_off, int
                 h[0] = f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
                 h[1] = f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16);
             }
-            *reinterpret_cast<u32x2*>((uint16_t*)p.C + i) = h;
+            asm_global_store_b64_wt((uint16_t*)p.C + i, h);
         }
         return;
     }
