@@ -426,6 +426,16 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const GemmArgs 
         v[0] = 0.0f;
         for (int s = 0; s < p.splits; ++s) v[0] += ws[s * mn];
     }
+    if constexpr (V == 4) {
+        // N % 4 == 0: the four elements share a row, and with vec_c they are
+        // one aligned 16-byte (fp32) or 8-byte (16-bit) piece of C
+        if (p.vec_c && p.N % 4 == 0) {
+            const int row = (int)(i0 / p.N), col = (int)(i0 - (int64_t)row * p.N);
+            const int64_t idx = (int64_t)b * p.sC + (int64_t)row * p.ldc + col;
+            store_c4(p, idx - col, col, (f32x4){v[0], v[1], v[2], v[3]});
+            return;
+        }
+    }
 #pragma unroll
     for (int e = 0; e < V; ++e) {
         const int64_t i = i0 + e;
