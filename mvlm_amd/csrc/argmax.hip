@@ -14,6 +14,7 @@
 #include "common.h"
 #include "device_math.h"
 
+#include <algorithm>
 #include <climits>
 
 namespace mvlm {
@@ -124,20 +125,132 @@ __global__ __launch_bounds__(ARGMAX_THREADS) void argmax_kernel(const void* x, i
     }
 }
 
+// Split form for a few long rows (the token pick: one row of 51200 logits took
+// 6.2-6.9 us on one workgroup, its key decode and compares on one CU's vector
+// ALUs).  Row `row` is cut into gridDim.x slices of whole 16-byte chunks, one
+// workgroup of ARGMAX_SPLIT_THREADS each (the last also takes the scalar
+// tail); each workgroup folds its (key, index) candidate into the row's 64-bit
+// word with a device-scope atomic max (the key, sign-flipped to order as an
+// unsigned number, in the high half; 0x7FFFFFFF - index in the low half, so
+// equal keys keep the smaller index) and, once that atomic has returned,
+// counts itself in on the row's arrival counter.  The workgroup that arrives
+// last reads the word, writes the index and sets word and counter back to
+// zero for the next launch (both live in the device's sync words, zero
+// between launches).
+constexpr int ARGMAX_SPLIT_THREADS = 256;
+constexpr int ARGMAX_SPLIT_ELEMS = 1600;    // elements per workgroup (about)
+constexpr int ARGMAX_SPLIT_MAX = 64;        // workgroups per row
+
+template <int DT, bool VEC>
+__global__ __launch_bounds__(ARGMAX_SPLIT_THREADS) void argmax_split_kernel(const void* x, int n, int64_t ld,
+                                                                             int* out, uint64_t* best,
+                                                                             uint32_t* arrived) {
+    __shared__ int wk[ARGMAX_SPLIT_THREADS / 64];
+    __shared__ int wi[ARGMAX_SPLIT_THREADS / 64];
+    constexpr int ES = DT == MVLM_F32 ? 4 : 2;
+    constexpr int EPC = 16 / ES;
+    const int row = (int)blockIdx.y, sl = (int)blockIdx.x, S = (int)gridDim.x;
+    const uint8_t* base = (const uint8_t*)x + (int64_t)row * ld * ES;
+    int bk = ARGMAX_NONE;
+    int bi = 0x7FFFFFFF;
+    // this slice: chunks [c0, c1) (VEC), else elements [e0, e1); the last
+    // slice also takes the elements past the last whole chunk
+    const int units = VEC ? n / EPC : n;
+    const int u0 = (int)((int64_t)units * sl / S), u1 = (int)((int64_t)units * (sl + 1) / S);
+    if constexpr (VEC) {
+        const u32x4* chunks = (const u32x4*)base;
+        for (int b0 = u0 + (int)threadIdx.x; b0 < u1; b0 += ARGMAX_SPLIT_THREADS * ARGMAX_BATCH) {
+            u32x4 c[ARGMAX_BATCH];
+#pragma unroll
+            for (int u = 0; u < ARGMAX_BATCH; ++u) c[u] = chunks[min(b0 + u * ARGMAX_SPLIT_THREADS, u1 - 1)];
+#pragma unroll
+            for (int u = 0; u < ARGMAX_BATCH; ++u) {
+                const int ci = b0 + u * ARGMAX_SPLIT_THREADS;
+                if (ci < u1) {
+#pragma unroll
+                    for (int e = 0; e < EPC; ++e) {
+                        const int k = argmax_key_bits<DT>(chunk_elem<DT>(c[u], e));
+                        if (k > bk) {
+                            bk = k;
+                            bi = ci * EPC + e;
+                        }
+                    }
+                }
+            }
+        }
+    }
+    const int e0 = VEC ? (sl == S - 1 ? units * EPC : n) : u0, e1 = VEC ? n : u1;
+    for (int i = e0 + (int)threadIdx.x; i < e1; i += ARGMAX_SPLIT_THREADS) {
+        const uint32_t b = ES == 4 ? ((const uint32_t*)base)[i] : ((const uint16_t*)base)[i];
+        const int k = argmax_key_bits<DT>(b);
+        if (k > bk) {
+            bk = k;
+            bi = i;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const int ok = __shfl_xor(bk, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (argmax_better(ok, oi, bk, bi)) {
+            bk = ok;
+            bi = oi;
+        }
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        wk[wave] = bk;
+        wi[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < ARGMAX_SPLIT_THREADS / 64; ++w)
+            if (argmax_better(wk[w], wi[w], bk, bi)) {
+                bk = wk[w];
+                bi = wi[w];
+            }
+        const uint64_t key = ((uint64_t)((uint32_t)bk ^ 0x80000000u) << 32) | (uint32_t)(0x7FFFFFFF - bi);
+        const uint64_t prev = __hip_atomic_fetch_max(best + row, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("" : : "v"(prev));      // the max has been performed before the count below
+        const uint32_t old = __hip_atomic_fetch_add(arrived + row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == (uint32_t)(S - 1)) {
+            const uint64_t w = __hip_atomic_load(best + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            out[row] = 0x7FFFFFFF - (int)(uint32_t)w;
+            __hip_atomic_store(best + row, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(arrived + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// slices per row of the split form, 1 for the one-workgroup form
+int argmax_splits(int rows, int n) {
+    if (rows > ARGMAX_SYNC_ROWS) return 1;
+    return std::min(ARGMAX_SPLIT_MAX, n / ARGMAX_SPLIT_ELEMS);
+}
+
 template <int DT>
-static void launch_dt(hipStream_t s, const void* x, int rows, int n, int64_t ld, int* out) {
+static void launch_dt(hipStream_t s, const void* x, int rows, int n, int64_t ld, int* out, void* sync) {
     constexpr int ES = DT == MVLM_F32 ? 4 : 2;
     const bool vec = ((uintptr_t)x & 15u) == 0 && (ld * ES) % 16 == 0;
+    const int S = sync ? argmax_splits(rows, n) : 1;
+    if (S > 1) {
+        uint64_t* best = (uint64_t*)sync;
+        uint32_t* arrived = (uint32_t*)(best + ARGMAX_SYNC_ROWS);
+        const dim3 grid((unsigned)S, (unsigned)rows), block(ARGMAX_SPLIT_THREADS);
+        if (vec) launch_kernel(argmax_split_kernel<DT, true>, grid, block, 0, s, x, n, ld, out, best, arrived);
+        else launch_kernel(argmax_split_kernel<DT, false>, grid, block, 0, s, x, n, ld, out, best, arrived);
+        return;
+    }
     const dim3 grid((unsigned)rows), block(ARGMAX_THREADS);
     if (vec) launch_kernel(argmax_kernel<DT, true>, grid, block, 0, s, x, n, ld, out);
     else launch_kernel(argmax_kernel<DT, false>, grid, block, 0, s, x, n, ld, out);
 }
 
-hipError_t launch_argmax(hipStream_t s, const void* x, int dtype, int rows, int n, int64_t ld, int* out) {
+hipError_t launch_argmax(hipStream_t s, const void* x, int dtype, int rows, int n, int64_t ld, int* out, void* sync) {
     switch (dtype) {
-        case MVLM_F32: launch_dt<MVLM_F32>(s, x, rows, n, ld, out); break;
-        case MVLM_F16: launch_dt<MVLM_F16>(s, x, rows, n, ld, out); break;
-        case MVLM_BF16: launch_dt<MVLM_BF16>(s, x, rows, n, ld, out); break;
+        case MVLM_F32: launch_dt<MVLM_F32>(s, x, rows, n, ld, out, sync); break;
+        case MVLM_F16: launch_dt<MVLM_F16>(s, x, rows, n, ld, out, sync); break;
+        case MVLM_BF16: launch_dt<MVLM_BF16>(s, x, rows, n, ld, out, sync); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -32,7 +32,15 @@ struct mvlm_device {
     // (MVLM_NOALLOC_SCRATCH_BYTES, noalloc.hip), used only by the entry points
     // that allocate nothing; resolved at device creation.
     void* noalloc_scratch = nullptr;
+    // Words of self-resetting cross-workgroup protocols (the split token
+    // pick's per-row best key and arrival count): zero between launches, each
+    // launch's last workgroup setting its words back.  Ops of one handle run in
+    // order on its stream, so they never share a word.  Allocated and zeroed
+    // at the first op that needs them.
+    void* sync_words = nullptr;
 };
+constexpr int ARGMAX_SYNC_ROWS = 64;                                   // rows of split token picks
+constexpr size_t SYNC_WORDS_BYTES = ARGMAX_SYNC_ROWS * (8 + 4);
 
 struct mvlm_buffer {
     mvlm_device* dev = nullptr;
@@ -104,6 +112,8 @@ inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
 // Device workspace of at least `bytes` (see mvlm_device::scratch_blocks).
 int device_scratch(mvlm_device* dev, size_t bytes, void** out);
+// The device's sync words (mvlm_device::sync_words), zeroed when first allocated.
+int device_sync_words(mvlm_device* dev, void** out);
 // Looks up the fixed workspace array's address on the current device
 // (noalloc.hip); sets dev->noalloc_scratch.
 int resolve_noalloc_scratch(mvlm_device* dev);
@@ -280,7 +290,11 @@ hipError_t launch_attention(hipStream_t s, const void* Q, const void* K, const v
                             int seq_q, int seq_kv, int heads, int head_dim, int causal, float scale, int num_cus,
                             void* workspace, size_t workspace_bytes);
 // row-wise argmax (first index of the largest key), one workgroup per row
-hipError_t launch_argmax(hipStream_t s, const void* x, int dtype, int rows, int n, int64_t ld, int* out);
+// sync: the device's sync words (device_sync_words), or null for the
+// one-workgroup-per-row form only
+hipError_t launch_argmax(hipStream_t s, const void* x, int dtype, int rows, int n, int64_t ld, int* out,
+                         void* sync = nullptr);
+int argmax_splits(int rows, int n);
 hipError_t launch_pack(hipStream_t s, const void* src, int dtype, int layout, int N, int K,
                        mvlm_weight* w);
 hipError_t launch_dequant(hipStream_t s, const mvlm_weight* w, float* out);

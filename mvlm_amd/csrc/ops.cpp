@@ -280,6 +280,7 @@ int make_argmax(mvlm_device* dev, const mvlm_buffer* x, int dtype, int rows, int
     op->a = x->ptr; op->c = out->ptr;
     op->a_dtype = dtype;
     op->M = rows; op->N = n; op->lda = ld;
+    if (argmax_splits(rows, n) > 1) return device_sync_words(dev, &op->workspace);
     return MVLM_OK;
 }
 
@@ -421,7 +422,7 @@ hipError_t enqueue_op(hipStream_t s, const Op& op, bool with_attn = false) {
             return launch_gemm_skinny(s, (const float*)op.a, op.w, (float*)op.c, op.M, op.N, op.K, op.num_cus,
                                       &op.ep);
         case OP_ARGMAX:
-            return launch_argmax(s, op.a, op.a_dtype, op.M, op.N, op.lda, (int*)op.c);
+            return launch_argmax(s, op.a, op.a_dtype, op.M, op.N, op.lda, (int*)op.c, op.workspace);
         case OP_ATTENTION:
             return launch_attention(s, op.a, op.b, op.v, op.c, op.c_dtype, op.M, op.N, op.batch, op.K, op.causal,
                                     op.scale, op.num_cus, op.workspace, op.workspace_bytes);

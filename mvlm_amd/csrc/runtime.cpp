@@ -133,6 +133,7 @@ extern "C" int mvlm_device_destroy(mvlm_device* dev) {
         if (st == MVLM_OK) st = st2;
     }
     for (void* p : dev->scratch_blocks) (void)hipFree(p);
+    if (dev->sync_words) (void)hipFree(dev->sync_words);
     delete dev;
     return st;
 }
@@ -158,6 +159,25 @@ int device_scratch(mvlm_device* dev, size_t bytes, void** out) {
         dev->scratch_bytes = want;
     }
     *out = dev->scratch_blocks.back();
+    return MVLM_OK;
+}
+
+int device_sync_words(mvlm_device* dev, void** out) {
+    if (!dev->sync_words) {
+        HIP_TRY(hipSetDevice(dev->ordinal));
+        void* p = nullptr;
+        if (hipMalloc(&p, SYNC_WORDS_BYTES) != hipSuccess || !p) {
+            (void)hipGetLastError();
+            return set_error(MVLM_ERR_OUT_OF_MEMORY, "sync word allocation failed");
+        }
+        if (hipMemsetAsync(p, 0, SYNC_WORDS_BYTES, dev->stream) != hipSuccess ||
+            hipStreamSynchronize(dev->stream) != hipSuccess) {
+            (void)hipFree(p);
+            return set_error(MVLM_ERR_HIP, "sync word initialisation failed");
+        }
+        dev->sync_words = p;
+    }
+    *out = dev->sync_words;
     return MVLM_OK;
 }
 }  // namespace mvlm
