@@ -152,6 +152,7 @@ struct StreamAttn {
     int consumers;             // mode 0: workgroups that wait for o
     int prod_rpb, prod_blocks; // mode 1: the producer problem's rows per workgroup and workgroups (first in the grid)
     float scale_log2;          // scale * log2(e)
+    uint32_t wait_ticks;       // bound of every wait, s_memrealtime ticks (ATTN_TIMEOUT)
 };
 
 struct StreamGroup {
@@ -223,7 +224,7 @@ __device__ __forceinline__ bool attn_wait_producers(const StreamAttn& a, int b, 
                 if (j <= (r0 + a.D - 1) / a.prod_rpb) up &= (int32_t)(sync_load(flags + j) - want) >= 0;
             }
             if (__builtin_amdgcn_ballot_w64(!up) == 0) break;
-            if (__builtin_amdgcn_s_memrealtime() - t0 > ATTN_TIMEOUT) {
+            if (__builtin_amdgcn_s_memrealtime() - t0 > (uint64_t)a.wait_ticks) {
                 ok = false;
                 break;
             }
@@ -517,7 +518,7 @@ __device__ __forceinline__ bool attn_wait(const StreamAttn& a, int wave, int lan
         uint32_t ok = 1;
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         while ((int32_t)(sync_load(go) - want) < 0) {
-            if (__builtin_amdgcn_s_memrealtime() - t0 > ATTN_TIMEOUT) {
+            if (__builtin_amdgcn_s_memrealtime() - t0 > (uint64_t)a.wait_ticks) {
                 ok = 0;
                 break;
             }
@@ -1034,6 +1035,10 @@ static bool attn_fill(StreamAttn& a, const StreamAttnDesc& d, int num_cus) {
     a.part_ml = a.part_o + (size_t)d.heads * a.splits * d.head_dim;
     a.blocks = d.heads * a.splits;
     a.scale_log2 = d.scale * 1.4426950408889634f;
+    // MVLM_ATTN_WAIT_TICKS shortens the bound (read at every launch; tests of
+    // the give-up path set it to 0 so that a wait gives up at its first poll)
+    a.wait_ticks = (uint32_t)ATTN_TIMEOUT;
+    if (const char* e = std::getenv("MVLM_ATTN_WAIT_TICKS")) a.wait_ticks = (uint32_t)std::strtoul(e, nullptr, 10);
     return a.blocks <= ATTN_MAX_BLOCKS;
 }
 

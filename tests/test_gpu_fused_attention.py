@@ -401,3 +401,52 @@ def test_decode_step_carried_by_the_readers_launch(dev, orc):
     ref.destroy()
     W3.free()
     c.free()
+
+
+def test_wait_give_up_is_reported_and_the_next_run_is_exact(dev, orc, monkeypatch):
+    """The give-up path of the bounded wait, forced from the host: with a wait
+    bound of 0 ticks (MVLM_ATTN_WAIT_TICKS, read at every launch of an eager
+    plan) a reader of o that polls before the attention is done gives up at
+    once; it stores NaN instead of its rows and sets the site's error word.
+    Every kernel still ends normally.  plan.check() reports the give-up and
+    clears the site's counters, and the next run with the normal bound is
+    bit-identical to the unfused plan's where it does not read o and within
+    tolerance where it does."""
+    c = Case(dev, m.Q8_0, 2048, 32, 64, 2048, 2048, 8192, 13)
+    ref = c.plan(dev, fuse=False)
+    ref.run(1)
+    ref.check()
+    o_ref, y1_ref, y2_ref = c.outputs()
+    p = c.plan(dev, fuse=True)
+    assert p.fused() == 1
+    monkeypatch.setenv("MVLM_ATTN_WAIT_TICKS", "0")
+    gave_up = 0
+    for r in range(5):
+        print(f"[give-up] forced run {r}", flush=True)
+        for b in (c.o, c.y1, c.y2):
+            b.zero()
+        p.run(1)
+        try:
+            p.check()
+        except m.native.MvlmError:
+            gave_up += 1
+            _, y1, y2 = c.outputs()
+            assert np.isnan(y1).any()                # the readers that gave up stored NaN
+            assert np.array_equal(y2, y2_ref)        # the rows that do not read o are untouched by it
+    assert gave_up > 0
+    monkeypatch.delenv("MVLM_ATTN_WAIT_TICKS")
+    for r in range(3):
+        print(f"[give-up] normal run {r}", flush=True)
+        for b in (c.o, c.y1, c.y2):
+            b.zero()
+        p.run(1)
+        p.check()
+        o, y1, y2 = c.outputs()
+        c.check_attention(orc, o)
+        assert np.all(np.isfinite(y1))
+        rows = np.unique(np.linspace(0, 2047, 128).astype(np.int64))
+        gemv_check(orc, o, c.W1, y1, rows, c.scratch)
+        assert np.array_equal(y2, y2_ref)
+    p.destroy()
+    ref.destroy()
+    c.free()
