@@ -808,6 +808,8 @@ def main():
                     help="only the prefill / vision GEMM shapes and the batched QK^T (one JSON line of them)")
     ap.add_argument("--gemm-bench", action="store_true",
                     help="only the reference bench's variant x config table (one JSON line)")
+    ap.add_argument("--latency-probe", action="store_true",
+                    help="first-load latency at kernel start (mvlm_probe_load_latency; one JSON line)")
     ap.add_argument("--barrier-probe", action="store_true",
                     help="software grid-barrier latency per round, each protocol with HBM idle and busy "
                          "(mvlm_probe_grid_barrier; one JSON line)")
@@ -855,6 +857,19 @@ def main():
                 res[key] = round(us, 2) if us != float("inf") else "gave up (a round > 20 ms)"
                 log(f"[bench]   grid barrier {name:24s} HBM {'busy' if bg else 'idle'}: {res[key]} us/round")
         print(json.dumps({"grid_barrier_us_per_round": res}), flush=True)
+        dev.close()
+        return
+    if args.latency_probe:
+        res = {}
+        for variant, vname in ((0, "from_hbm"), (1, "out_of_range")):
+            for after in (0, 4, 9):
+                runs = [dev.probe_load_latency(variant, after) for _ in range(3)]
+                best = min(runs, key=lambda r: r[1])
+                key = f"{vname}_after{after}"
+                res[key] = {"min_us": best[0], "median_us": best[1], "p90_us": best[2], "max_us": best[3]}
+                log(f"[bench]   first load {vname:12s} with {after} behind: min {best[0]:.2f} median {best[1]:.2f} "
+                    f"p90 {best[2]:.2f} max {best[3]:.2f} us")
+        print(json.dumps({"first_load_latency": res}), flush=True)
         dev.close()
         return
     if args.gemm_bench:

@@ -428,6 +428,16 @@ int mvlm_marker_elapsed_ms(mvlm_event* start, mvlm_event* end, float* ms);
  * (512 MiB with background). */
 int mvlm_probe_grid_barrier(mvlm_device* dev, int variant, int rounds, int background, double* us_per_round);
 
+/* Load latency at the start of a kernel (no counterpart in the reference: the
+ * measurement behind the small-K product's loads).  One workgroup of 16 waves
+ * per CU; each wave times one 16-byte-per-lane buffer load from its issue to
+ * its return with s_memrealtime: variant 0 reads lines of a freshly written
+ * 1 GiB buffer (from HBM), variant 1 an offset past the buffer's size (zeros,
+ * no data moved); `after` (0, 4 or 9) more loads of the wave are issued behind
+ * it.  us[0..3] = min, median, 90th percentile and max over the waves, in
+ * microseconds.  Synchronous; allocates 1 GiB. */
+int mvlm_probe_load_latency(mvlm_device* dev, int variant, int after, double* us);
+
 #ifdef __cplusplus
 }
 #endif

@@ -145,8 +145,9 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm_smallk_kernel(const SmallK
 
     // 1. the first A groups of this thread, then every B fragment of this wave
     //    (columns of blocks past `mine` load column N - 1 and are never stored)
-    //    (a wave with no A group left loads nothing: an out-of-range load took
-    //    ~2.4 us to return zeros here, a load from memory ~0.4 us)
+    //    (a wave with no A group left loads nothing: its one load would wait
+    //    behind the other waves' loads in the CU's queue, ~2.4 us in the
+    //    stamped copy, and the barrier after the staging waits for every wave)
     u32x4 ae[SK_A_EARLY];
 #pragma unroll
     for (int u = 0; u < SK_A_EARLY; ++u) {

@@ -17,6 +17,7 @@
 // rounds and is reported as MVLM_ERR_HIP.
 #include "common.h"
 
+#include <algorithm>
 #include <vector>
 
 namespace mvlm {
@@ -114,9 +115,86 @@ __global__ __launch_bounds__(576, 1) void probe_barrier_kernel(ProbeArgs a) {
     }
 }
 
+// Load latency at the start of a kernel (mvlm_probe_load_latency): one
+// workgroup of 16 waves per CU; every wave stamps s_memrealtime, issues one
+// 16-byte-per-lane buffer load (variant 0: inside the buffer; variant 1: at an
+// offset past the buffer's size, which returns zeros and moves no data), then
+// `after` more in-range loads of its own (traffic queued behind the probe),
+// waits for the probe load only and stamps again.  The buffer is 1 GiB,
+// written once before the launch, and the probe reads its first 64 MiB, so
+// the lines come from HBM.
+struct LatArgs {
+    const uint8_t* buf;
+    uint32_t buf_bytes;
+    uint32_t* ticks;           // [nb * 16]
+    int variant, after;
+};
+
+template <int AFTER>
+__global__ __launch_bounds__(1024, 1) void probe_latency_kernel(LatArgs a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int w = blockIdx.x * 16 + wave;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.buf), 0, (int)a.buf_bytes,
+                                                                       0x00020000);
+    const uint32_t base = (uint32_t)(w * 64 + lane) * 16;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    const uint32_t off = a.variant == 1 ? 0x7FFFFFF0u : base;
+    p32x4 v = __builtin_bit_cast(p32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    p32x4 extra[AFTER > 0 ? AFTER : 1];
+#pragma unroll
+    for (int u = 0; u < AFTER; ++u)
+        extra[u] = __builtin_bit_cast(p32x4, __builtin_amdgcn_raw_buffer_load_b128(r, base + (uint32_t)(u + 1) * (16u << 20), 0, 0));
+    // the probe load is the oldest: the compiler's wait for v leaves AFTER in flight
+    asm volatile("" : "+v"(v));
+    const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
+    p32x4 acc = v;
+#pragma unroll
+    for (int u = 0; u < AFTER; ++u) acc ^= extra[u];
+    const uint32_t mix = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];   // every loaded byte is used
+    if (lane == 0) a.ticks[w] = (uint32_t)(t1 - t0) | (mix == 0x9E3779B9u ? 0x80000000u : 0u);
+}
+
 }  // namespace mvlm
 
 using namespace mvlm;
+
+extern "C" int mvlm_probe_load_latency(mvlm_device* dev, int variant, int after, double* us) {
+    REQUIRE(dev && us, "mvlm_probe_load_latency: null argument");
+    REQUIRE(variant == 0 || variant == 1, "mvlm_probe_load_latency: variant %d not 0 or 1", variant);
+    REQUIRE(after == 0 || after == 4 || after == 9, "mvlm_probe_load_latency: after %d not 0, 4 or 9", after);
+    HIP_TRY(hipSetDevice(dev->ordinal));
+    const int nb = dev->prop.multiProcessorCount;
+    const size_t buf_bytes = (size_t)1 << 30;
+    // in-range offsets: wave w's lanes at w KiB, its loads 16 MiB apart (at most
+    // nb * 16 KiB + 9 * 16 MiB + 1 KiB < 1 GiB)
+    REQUIRE((size_t)nb * 16 * 1024 + 10 * ((size_t)16 << 20) < buf_bytes, "mvlm_probe_load_latency: too many CUs");
+    uint8_t* buf = nullptr;
+    uint32_t* ticks = nullptr;
+    HIP_TRY(hipMalloc(&buf, buf_bytes));
+    int st = check_hip(hipMalloc(&ticks, (size_t)nb * 16 * 4), "probe alloc");
+    if (st == MVLM_OK) st = check_hip(hipMemsetAsync(buf, 0x5A, buf_bytes, dev->stream), "probe memset");
+    LatArgs a{buf, (uint32_t)(buf_bytes - 1), ticks, variant, after};
+    if (st == MVLM_OK) {
+        if (after == 0) hipLaunchKernelGGL(probe_latency_kernel<0>, dim3(nb), dim3(1024), 0, dev->stream, a);
+        else if (after == 4) hipLaunchKernelGGL(probe_latency_kernel<4>, dim3(nb), dim3(1024), 0, dev->stream, a);
+        else hipLaunchKernelGGL(probe_latency_kernel<9>, dim3(nb), dim3(1024), 0, dev->stream, a);
+        st = check_hip(hipGetLastError(), "probe launch");
+    }
+    if (st == MVLM_OK) st = check_hip(hipStreamSynchronize(dev->stream), "probe sync");
+    std::vector<uint32_t> t((size_t)nb * 16);
+    if (st == MVLM_OK) st = check_hip(hipMemcpy(t.data(), ticks, t.size() * 4, hipMemcpyDeviceToHost), "probe read");
+    (void)hipFree(buf);
+    if (ticks) (void)hipFree(ticks);
+    if (st != MVLM_OK) return st;
+    for (uint32_t& x : t) x &= 0x7FFFFFFFu;
+    std::sort(t.begin(), t.end());
+    const size_t n = t.size();
+    us[0] = t[0] / 100.0;                       // s_memrealtime: 100 MHz
+    us[1] = t[n / 2] / 100.0;
+    us[2] = t[(n * 9) / 10] / 100.0;
+    us[3] = t[n - 1] / 100.0;
+    return MVLM_OK;
+}
 
 extern "C" int mvlm_probe_grid_barrier(mvlm_device* dev, int variant, int rounds, int background,
                                        double* us_per_round) {

@@ -107,6 +107,7 @@ _SIGNATURES = {
     "mvlm_gemv_ex": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, c_int, POINTER(Epilogue), _PP]),
     "mvlm_gemm_packed_ex_noalloc": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, c_int, c_int, POINTER(Epilogue)]),
     "mvlm_probe_grid_barrier": (c_int, [_P, c_int, c_int, c_int, POINTER(c_double)]),
+    "mvlm_probe_load_latency": (c_int, [_P, c_int, c_int, POINTER(c_double)]),
     "mvlm_plan_add_gemv_ex": (c_int, [_P, _P, c_int, _P, _P, c_int, POINTER(Epilogue)]),
     "mvlm_plan_add_gemm_packed_ex": (c_int, [_P, _P, c_int, _P, _P, c_int, c_int, POINTER(Epilogue)]),
     "mvlm_plan_add_gemv_grouped": (c_int, [_P, c_int, POINTER(GemvDesc)]),
@@ -643,6 +644,12 @@ class Device:
         us = c_double()
         _call("mvlm_probe_grid_barrier", self.handle, variant, rounds, 1 if background else 0, byref(us))
         return us.value
+
+    def probe_load_latency(self, variant: int, after: int) -> list:
+        """[min, median, p90, max] microseconds of a wave's first load (mvlm_probe_load_latency)"""
+        us = (c_double * 4)()
+        _call("mvlm_probe_load_latency", self.handle, variant, after, us)
+        return list(us)
 
     def gemv_ex(self, x, x_dtype, W, y, y_dtype, N, K, bias=None, act=ACT_NONE, mul=None, residual=None,
                 event=False):
