@@ -690,6 +690,16 @@ def test_gemm_forced_k_splits(dev, orc, monkeypatch, splits, M, N, K, ab, cd):
     check_packed(dev, orc, M, N, K, ab, cd, seed=300 + int(splits))
 
 
+@pytest.mark.parametrize("tile", ["256x256s2w8", "256x128s2w8", "192x128s3w8", "128x128s4w8", "64x64s4w4",
+                                  "128x128s2w8k128", "64x64s2w4k128", "192x128s2w8k128", "96x192s2w6k128"])
+@pytest.mark.parametrize("M,N,K,ab,cd", [(300, 410, 1000, F16, F32), (97, 200, 264, BF16, BF16)])
+def test_gemm_every_automatic_tile(dev, orc, monkeypatch, tile, M, N, K, ab, cd):
+    """each tile the planner can choose, forced, on shapes that leave partial
+    tiles along M and N and a K tail past the last full stage"""
+    monkeypatch.setenv("MVLM_GEMM_TILE", tile)
+    check_packed(dev, orc, M, N, K, ab, cd, seed=320)
+
+
 def test_gemm_k_splits_with_epilogue_and_batches(dev, orc, monkeypatch):
     from test_gpu_epilogue import check as ep_check, make_operands
     from mvlm_amd import native
