@@ -605,7 +605,7 @@ def pmc_probe(steps=3):
 
 
 PMC_WORKLOADS = ("decode_q8_0_m1", "decode_q4_0_m1", "decode_q4_0_m4", "decode_q4_0_m16", "decode_q8_0_m4", "gemm",
-                 "gemm_bf16", "gemv_f32", "gemv_exact", "qk_batched", "attention", "argmax", "token")
+                 "gemm_bf16", "gemm_vendor", "gemv_f32", "gemv_exact", "qk_batched", "attention", "argmax", "token")
 
 
 def pmc_workload(name, reps=2):
@@ -675,6 +675,22 @@ def pmc_workload(name, reps=2):
         plan, ws, _ = build_token_plan(dev, m, "q8_0", 512, True)
         plans.append((name, plan))
         weights += ws
+    elif name == "gemm_vendor":   # torch.matmul (the vendor library) on the Phi-1.5 QKV and fc1 shapes
+        class Vendor:
+            def __init__(self, M, N, K):
+                g = torch.Generator(device="cuda").manual_seed(SEED)
+                self.A = torch.randn(M, K, device="cuda", dtype=torch.float16, generator=g)
+                self.W = torch.randn(N, K, device="cuda", dtype=torch.float16, generator=g) * 0.02
+
+            def run(self, n):
+                for _ in range(n):
+                    torch.matmul(self.A, self.W.t())
+                torch.cuda.synchronize()
+
+            def destroy(self):
+                pass
+        for wname, M, N, K in GEMM_SHAPES[:2]:
+            plans.append((wname, Vendor(M, N, K)))
     elif name == "argmax":
         n = PHI_LM_HEAD[1]
         x = dev.fill_normal(dev.alloc(n * 4), m.F32, n, SEED ^ 0x601, 1.0)
