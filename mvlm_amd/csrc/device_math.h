@@ -232,6 +232,27 @@ __device__ __forceinline__ void asm_global_load_lds_b128(const void* gaddr, uint
 }
 #pragma clang diagnostic pop
 
+// The buffer-addressed form of the same direct load: lane i's 16 bytes at
+// byte voff of the buffer described by rsrc (four wave-uniform words: base,
+// base high | stride 0, size in bytes, format) land at LDS byte
+// lds_base + 16 * i.  A 32-bit offset per lane instead of a 64-bit address.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 raw_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    return i32x4{(int)__builtin_amdgcn_readfirstlane((uint32_t)a),
+                 (int)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xFFFFu),
+                 (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000};
+}
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void asm_buffer_load_lds_b128(i32x4 rsrc, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :
+                 : "v"(voff), "s"(rsrc), "s"(lds_base)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 // A 16-byte global load the compiler does not track (wait with
 // asm_wait_vmcnt, then asm_pin the result).
 __device__ __forceinline__ u32x4 asm_global_load_b128(const void* p) {

@@ -162,6 +162,26 @@ __device__ __forceinline__ void stage_direct(const uint16_t* __restrict__ base, 
     }
 }
 
+// stage_direct through a buffer descriptor whose base is the tile's first row:
+// a 32-bit offset per lane instead of a 64-bit address (fewer VGPRs, and the
+// Phi-1.5 M = 768 shapes and 4096^3 2-5% faster; the SigLIP tiles keep the
+// global form, which measured as fast or faster there)
+template <int BK, int ROWS, int NW>
+__device__ __forceinline__ void stage_direct_buf(i32x4 rsrc, int64_t ld, int r0, int rmax, int k0, uint16_t* lds,
+                                                 int wave, int lane) {
+    using G = StageGeom<BK>;
+    static_assert((ROWS / G::RPI) % NW == 0, "row groups must split evenly over the waves");
+#pragma unroll
+    for (int t = 0; t < ROWS / (G::RPI * NW); ++t) {
+        const int g = wave + NW * t;
+        const int lr = G::RPI * g + lane / G::LPR;
+        const int ls = (lane % G::LPR) ^ G::swz(lr);
+        const int r = min(r0 + lr, rmax) - r0;
+        const uint32_t off = (uint32_t)(((int64_t)r * ld + k0 + ls * 8) * 2);
+        asm_buffer_load_lds_b128(rsrc, off, __builtin_amdgcn_readfirstlane(lds_offset(lds + G::RPI * g * G::ROWH)));
+    }
+}
+
 // Guarded loads of the last stage: 16-byte chunks at or beyond kread are zero.
 template <int BK, int ROWS, int NW>
 __device__ __forceinline__ void stage_guarded(const uint16_t* __restrict__ base, int64_t ld, int r0, int rmax, int k0,
@@ -181,7 +201,7 @@ __device__ __forceinline__ void stage_guarded(const uint16_t* __restrict__ base,
     }
 }
 
-template <bool BF16, int BM, int BN, int BK, int STAGES, int WGM, int WGN>
+template <bool BF16, int BM, int BN, int BK, int STAGES, int WGM, int WGN, bool BUF>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(const GemmArgs p) {
     using G = StageGeom<BK>;
     constexpr int ROWH = G::ROWH;
@@ -219,14 +239,20 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(const GemmArg
     const bool tail_a = (nk_all * BK > K) && kt0 + nk == nk_all;
     const bool tail_b = (nk_all * BK > p.kread_b) && kt0 + nk == nk_all;
 
+    // BUF: descriptors over the tile's rows of A and B (every offset stays below
+    // the 32-bit size, checked by the launcher)
+    const i32x4 ra = raw_rsrc(A + (int64_t)m0 * p.lda, BUF ? (uint32_t)((int64_t)(p.M - m0) * p.lda * 2) : 0u);
+    const i32x4 rb = raw_rsrc(B + (int64_t)n0 * p.ldb, BUF ? (uint32_t)((int64_t)(p.N - n0) * p.ldb * 2) : 0u);
     auto issue = [&](int kt) {
         uint16_t* slot = smem + (kt % STAGES) * SLOT;
         const int k0 = (kt0 + kt) * BK;
         const bool last = (kt == nk - 1);
         if (last && tail_a) stage_guarded<BK, BM, NW>(A, p.lda, m0, p.M - 1, k0, K, slot, wave, lane);
+        else if constexpr (BUF) stage_direct_buf<BK, BM, NW>(ra, p.lda, m0, p.M - 1, k0, slot, wave, lane);
         else stage_direct<BK, BM, NW>(A, p.lda, m0, p.M - 1, k0, slot, wave, lane);
         if (last && tail_b)
             stage_guarded<BK, BN, NW>(B, p.ldb, n0, p.N - 1, k0, p.kread_b, slot + BM * ROWH, wave, lane);
+        else if constexpr (BUF) stage_direct_buf<BK, BN, NW>(rb, p.ldb, n0, p.N - 1, k0, slot + BM * ROWH, wave, lane);
         else stage_direct<BK, BN, NW>(B, p.ldb, n0, p.N - 1, k0, slot + BM * ROWH, wave, lane);
     };
 
@@ -453,12 +479,15 @@ struct TileCfg {
     int bm, bn, bk, stages, waves;
     int per_cu;       // resident blocks per CU (LDS ring and registers)
     int eff;          // TFLOP/s of a full-wave 4096^3 fp16 run (selection weight)
+    bool buf;         // buffer-addressed direct loads: operands below 4 GiB only
     GemmKernel f16, bf16;
 };
 
-#define MVLM_TILE(BMv, BNv, BKv, Sv, WMv, WNv, PER_CU, EFF)                                          \
-    TileCfg{BMv, BNv, BKv, Sv, WMv * WNv, PER_CU, EFF, gemm_mfma_kernel<false, BMv, BNv, BKv, Sv, WMv, WNv>, \
-            gemm_mfma_kernel<true, BMv, BNv, BKv, Sv, WMv, WNv>}
+#define MVLM_TILE_X(BMv, BNv, BKv, Sv, WMv, WNv, PER_CU, EFF, BUFv)                                         \
+    TileCfg{BMv, BNv, BKv, Sv, WMv * WNv, PER_CU, EFF, BUFv, gemm_mfma_kernel<false, BMv, BNv, BKv, Sv, WMv, WNv, BUFv>, \
+            gemm_mfma_kernel<true, BMv, BNv, BKv, Sv, WMv, WNv, BUFv>}
+#define MVLM_TILE(BMv, BNv, BKv, Sv, WMv, WNv, PER_CU, EFF) MVLM_TILE_X(BMv, BNv, BKv, Sv, WMv, WNv, PER_CU, EFF, false)
+#define MVLM_TILE_B(BMv, BNv, BKv, Sv, WMv, WNv, PER_CU, EFF) MVLM_TILE_X(BMv, BNv, BKv, Sv, WMv, WNv, PER_CU, EFF, true)
 // The first nine are the automatic choices (eff measured at 4096^3, fp16 in,
 // fp32 out); the others are kept for tuning.  The 128-wide stages halve a
 // block's stage count (and its waits and barriers), which pays on the short-K
@@ -469,11 +498,11 @@ struct TileCfg {
 // few-row products.  96 x 192 with six waves of 32 x 96 cuts 768 x 6144 into
 // exactly 256 blocks (192 with 192 x 128): 35.4 -> 34.3 us at that shape.
 static const TileCfg kTiles[] = {
-    MVLM_TILE(256, 256, 64, 2, 4, 2, 1, 907), MVLM_TILE(256, 128, 64, 2, 4, 2, 1, 785),
-    MVLM_TILE(192, 128, 64, 3, 2, 4, 1, 636), MVLM_TILE(128, 128, 64, 4, 4, 2, 1, 619),
+    MVLM_TILE_B(256, 256, 64, 2, 4, 2, 1, 907), MVLM_TILE_B(256, 128, 64, 2, 4, 2, 1, 785),
+    MVLM_TILE_B(192, 128, 64, 3, 2, 4, 1, 636), MVLM_TILE(128, 128, 64, 4, 4, 2, 1, 619),
     MVLM_TILE(64, 64, 64, 4, 2, 2, 2, 401), MVLM_TILE(128, 128, 128, 2, 4, 2, 1, 682),
-    MVLM_TILE(64, 64, 128, 2, 2, 2, 2, 460), MVLM_TILE(192, 128, 128, 2, 2, 4, 1, 700),
-    MVLM_TILE(96, 192, 128, 2, 3, 2, 1, 564),
+    MVLM_TILE(64, 64, 128, 2, 2, 2, 2, 460), MVLM_TILE_B(192, 128, 128, 2, 2, 4, 1, 700),
+    MVLM_TILE_B(96, 192, 128, 2, 3, 2, 1, 564),
     MVLM_TILE(256, 128, 64, 3, 4, 2, 1, 628), MVLM_TILE(128, 128, 64, 4, 2, 2, 1, 502),
     MVLM_TILE(128, 64, 64, 4, 2, 2, 1, 375),
     MVLM_TILE(256, 256, 32, 4, 4, 2, 1, 849), MVLM_TILE(256, 256, 32, 5, 4, 2, 1, 828),
@@ -482,6 +511,8 @@ static const TileCfg kTiles[] = {
 };
 constexpr int kAutoTiles = 9;
 #undef MVLM_TILE
+#undef MVLM_TILE_B
+#undef MVLM_TILE_X
 
 struct GemmPlan {
     const TileCfg* tile;
@@ -494,8 +525,8 @@ struct GemmPlan {
 // second launch.  MVLM_GEMM_TILE=<bm>x<bn>s<stages>w<waves>[k<bk>] forces a
 // compiled tile and MVLM_GEMM_SPLITS=<n> a split count (tuning runs; read at
 // every launch).
-static GemmPlan plan_gemm(int M, int N, int K, int batch, int num_cus) {
-    GemmPlan best{&kTiles[kAutoTiles - 1], 1, 0};
+static GemmPlan plan_gemm(int M, int N, int K, int batch, int num_cus, bool buf_ok) {
+    GemmPlan best{&kTiles[4], 1, 0};
     double best_t = 1e30;
     const char* force = std::getenv("MVLM_GEMM_TILE");
     const TileCfg* forced = nullptr;
@@ -503,7 +534,8 @@ static GemmPlan plan_gemm(int M, int N, int K, int batch, int num_cus) {
         int bm = 0, bn = 0, st = 0, w = 0, bk = 64;
         if (std::sscanf(force, "%dx%ds%dw%dk%d", &bm, &bn, &st, &w, &bk) >= 4)
             for (const TileCfg& c : kTiles)
-                if (c.bm == bm && c.bn == bn && c.stages == st && c.waves == w && c.bk == bk) forced = &c;
+                if (c.bm == bm && c.bn == bn && c.stages == st && c.waves == w && c.bk == bk && (buf_ok || !c.buf))
+                    forced = &c;
     }
     const char* fs = std::getenv("MVLM_GEMM_SPLITS");
     const int forced_splits = fs ? std::atoi(fs) : 0;
@@ -517,6 +549,7 @@ static GemmPlan plan_gemm(int M, int N, int K, int batch, int num_cus) {
     const int n_cand = forced ? 1 : kAutoTiles;
     for (int i = 0; i < n_cand; ++i) {
         const TileCfg& c = forced ? *forced : kTiles[i];
+        if (c.buf && !buf_ok) continue;
         const int nk = (K + c.bk - 1) / c.bk;
         for (int splits : {1, 2, 3, 4, 6, 8}) {
             if (forced_splits > 0 && splits != forced_splits) continue;
@@ -568,7 +601,10 @@ static GemmWorkspace gemm_workspace(int batch, int M, int N, int K, int64_t lda,
     w.pad_a = K % 8 != 0 || lda % 8 != 0 || (batch > 1 && sA % 8 != 0);
     w.pad_b = ldb % 8 != 0 || (batch > 1 && sB % 8 != 0) || kread_b < k8;
     w.kp = (w.pad_a || w.pad_b) ? k8 : K;
-    w.plan = plan_gemm(M, N, w.kp, batch, num_cus > 0 ? num_cus : 256);
+    // buffer-addressed tiles need each operand's rows within a 32-bit byte range
+    const int64_t lda_k = w.pad_a ? w.kp : lda, ldb_k = w.pad_b ? w.kp : ldb;
+    const bool buf_ok = (int64_t)M * lda_k * 2 < ((int64_t)1 << 32) - 256 && (int64_t)N * ldb_k * 2 < ((int64_t)1 << 32) - 256;
+    w.plan = plan_gemm(M, N, w.kp, batch, num_cus > 0 ? num_cus : 256, buf_ok);
     w.split_bytes = w.plan.splits > 1 ? align256((size_t)w.plan.splits * batch * M * N * sizeof(float)) : 0;
     w.a_off = w.split_bytes;
     const size_t a_bytes = w.pad_a ? align256((size_t)batch * M * w.kp * 2) : 0;
