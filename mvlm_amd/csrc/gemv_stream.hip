@@ -601,13 +601,17 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
     const int row0 = rb0 + (wave / SPLIT) * R;
     const bool active = row0 < rb1;
 
-    // the codes: every load of this wave before any arithmetic
-    const uint8_t* rowp[R];
+    // the codes: every load of this wave before any arithmetic, through a
+    // buffer descriptor (32-bit offsets: the host keeps a weight's codes below
+    // 4 GiB on this path)
+    const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(P.codes), 0, (int)min((int64_t)P.N * P.ld_bytes, (int64_t)0x7FFFFFFF), 0x00020000);
+    uint32_t rowo[R];
     int srow[R];                                      // row's scale byte offset in the staged region
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int64_t row = (int64_t)min(row0 + r, rb1 - 1);
-        rowp[r] = P.codes + row * P.ld_bytes;
+        rowo[r] = (uint32_t)(row * P.ld_bytes);
         srow[r] = (int)(row * (nb * 2) - s_base);
     }
     u32x4 q[R][CW];
@@ -621,7 +625,8 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
         kk[i] = k < K ? k : 0;
 #pragma unroll
         for (int r = 0; r < R; ++r)
-            q[r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rowp[r] + (int64_t)kk[i] * 16 / WPL));
+            q[r][i] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(cr, (int)(rowo[r] + (uint32_t)(kk[i] * 16 / WPL)), 0, 2));
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -914,6 +919,7 @@ bool stream_supported(const mvlm_weight* w, int M) {
     const int shape = stream_shape(w, M, 0);
     if (M > 1 && (M > 4 || !is_quant(w->dtype))) return false;
     return shape >= 0 && w->K % weight_wpl(w->dtype) == 0 &&
+           w->bytes <= 0x7FFFFFFF &&   // 32-bit code offsets of the buffer loads
            stream_lds_bytes(w, MVLM_F32, shape, batch_mx(M)) <= STREAM_LDS_MAX;
 }
 
