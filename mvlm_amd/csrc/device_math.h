@@ -253,6 +253,13 @@ __device__ __forceinline__ void asm_buffer_load_lds_b128(i32x4 rsrc, uint32_t vo
 }
 #pragma clang diagnostic pop
 
+// A 16-byte buffer load the compiler does not track (wait with
+// asm_wait_vmcnt, then asm_pin the result).
+__device__ __forceinline__ u32x4 asm_buffer_load_b128(i32x4 rsrc, uint32_t voff) {
+    u32x4 v;
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(rsrc) : "memory");
+    return v;
+}
 // A 16-byte global load the compiler does not track (wait with
 // asm_wait_vmcnt, then asm_pin the result).
 __device__ __forceinline__ u32x4 asm_global_load_b128(const void* p) {

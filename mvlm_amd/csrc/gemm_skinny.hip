@@ -202,8 +202,13 @@ __global__ __launch_bounds__(64 * NW, 4) void gemm_skinny_kernel(const SkinnyGro
         __builtin_amdgcn_global_load_lds(scale_bytes_ptr + off, (lds_void*)(lds + piece * 256), 4, 0, 0);
     }
 
-    // one step's direct loads: this wave's code rows into slot (step & 1)
-    const float* xrow = X + (int64_t)min(l16, M - 1) * K + 8 * q;
+    // one step's direct loads: this wave's code rows into slot (step & 1).
+    // Codes and X are read through buffer descriptors (32-bit offsets; the
+    // host keeps both below 2 GiB on this path).
+    const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(codes), 0, (int)min((int64_t)N * ld, (int64_t)0x7FFFFFFF), 0x00020000);
+    const i32x4 xrs = raw_rsrc(X, (uint32_t)((int64_t)M * K * 4));
+    const uint32_t xrow = (uint32_t)(((int64_t)min(l16, M - 1) * K + 8 * q) * 4);
     const int dma_row = lane / L::P, dma_piece = lane % L::P;
     auto issue_codes = [&](int step, int slot_idx) {
         const int kb = b0 + step * G;
@@ -213,7 +218,7 @@ __global__ __launch_bounds__(64 * NW, 4) void gemm_skinny_kernel(const SkinnyGro
             const int r = t * L::RPI + dma_row;
             const int64_t row = min(n0 + r, N - 1);
             const int64_t off = min((int64_t)kb * L::BB + 16 * L::piece(dma_piece, r), row_bytes - 16);
-            __builtin_amdgcn_global_load_lds(codes + row * ld + off, (lds_void*)(slot + t * 1024), 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(crs, (lds_void*)(slot + t * 1024), 16, (int)(row * ld + off), 0, 0, 0);
         }
     };
     // X of block g of one step into registers.  A lane's 8 floats are two
@@ -229,8 +234,8 @@ __global__ __launch_bounds__(64 * NW, 4) void gemm_skinny_kernel(const SkinnyGro
     const int xsw = xodd ? 4 : 0;
     auto load_x = [&](int step, int g, u32x4 (&xg)[2]) {
         const int bb = min(b0 + step * G + g, nb - 1);
-        xg[0] = asm_global_load_b128(xrow + 32 * bb + xsw);
-        xg[1] = asm_global_load_b128(xrow + 32 * bb + 4 - xsw);
+        xg[0] = asm_buffer_load_b128(xrs, xrow + (uint32_t)(32 * bb + xsw) * 4);
+        xg[1] = asm_buffer_load_b128(xrs, xrow + (uint32_t)(32 * bb + 4 - xsw) * 4);
     };
 
     // Lanes whose X row is past M (clamped to row M - 1 above) only feed
@@ -415,6 +420,7 @@ bool skinny_supported(int count, const mvlm_weight* const* ws, int num_cus) {
     for (int i = 0; i < count; ++i) {
         const mvlm_weight* w = ws[i];
         if (!is_quant(w->dtype) || w->K % 32 != 0) return false;
+        if (w->bytes > 0x7FFFFFFF || (int64_t)16 * w->K * 4 > 0x7FFFFFFF) return false;   // 32-bit buffer offsets
         const size_t lds = w->dtype == MVLM_Q4_0 ? skinny_lds_for<true>(sh, w->K) : skinny_lds_for<false>(sh, w->K);
         if (lds > SKINNY_LDS_MAX) return false;
     }
