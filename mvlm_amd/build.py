@@ -12,6 +12,7 @@ from __future__ import annotations
 import argparse
 import concurrent.futures as cf
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -42,19 +43,43 @@ def sources():
     return srcs
 
 
+def _stack_kernels(remarks: str) -> list:
+    """Kernels whose private (scratch) memory is more than their register
+    spills explain, from the compiler's kernel-resource-usage remarks: an
+    array the compiler could not keep in registers (a dynamically indexed
+    one) lands in scratch memory and costs every access a memory round trip."""
+    bad = []
+    for block in remarks.split("Function Name: ")[1:]:
+        name = block.split()[0]
+        def val(key):
+            m = re.search(re.escape(key) + r": (\d+)", block)
+            return int(m.group(1)) if m else 0
+        scratch = val("ScratchSize [bytes/lane]")
+        spills = val("VGPRs Spill") + val("SGPRs Spill")
+        if scratch > 4 * spills + 16:
+            bad.append(f"{name}: {scratch} bytes of scratch per lane, {spills} spilled registers")
+    return bad
+
+
 def _compile(src: str) -> str:
     obj = _object(src)
     cmd = [HIPCC, f"--offload-arch={ARCH}", *COMMON]
     if src.endswith(".hip"):
-        cmd += ["-x", "hip", *DEVICE_FLAGS]
+        cmd += ["-x", "hip", *DEVICE_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-fno-caret-diagnostics"]
     cmd += ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
-    msgs = "\n".join(l for l in (r.stdout + r.stderr).splitlines()
-                     if "packed-fp32-ops' is not a recognized feature" not in l)
+    out = r.stdout + r.stderr
+    msgs = "\n".join(l for l in out.splitlines()
+                     if "packed-fp32-ops' is not a recognized feature" not in l and "remark:" not in l
+                     and "-Rpass-analysis=kernel-resource-usage" not in l)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{msgs}")
     if msgs.strip():
         print(msgs, file=sys.stderr)
+    bad = _stack_kernels("\n".join(l.split("remark: ", 1)[1] for l in out.splitlines() if "remark: " in l))
+    if bad:
+        os.remove(obj)
+        raise RuntimeError(f"{src}: kernels with scratch memory beyond their register spills:\n  " + "\n  ".join(bad))
     return obj
 
 

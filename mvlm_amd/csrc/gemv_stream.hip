@@ -338,18 +338,25 @@ __device__ __forceinline__ void attn_decode_block(const StreamAttn& a, int b, fl
     };
     // the first iteration's cached keys and values, requested before q (they
     // do not depend on the producers)
+    // (through buffer descriptors: 32-bit offsets, the caches being checked
+    // below 2 GiB on the host)
     u32x4 kr[ATTN_NL], vr[ATTN_NL];
     int base = k0 + wave * KPW;
+    const int cache_bytes = (int)((int64_t)(a.cached + 1) * key_stride * 2);
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(a.k, 0, cache_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(a.v, 0, cache_bytes, 0x00020000);
     auto load_kv = [&](int at) {
 #pragma unroll
         for (int j = 0; j < ATTN_NL; ++j) {
-            const int64_t r = min(at + j * KPI + kl, kc1 - 1);
-            kr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.k + r * key_stride + col));
+            const int r = min(at + j * KPI + kl, kc1 - 1);
+            kr[j] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, (int)((r * key_stride + col) * 2), 0, 2));
         }
 #pragma unroll
         for (int j = 0; j < ATTN_NL; ++j) {
-            const int64_t r = min(at + j * KPI + kl, kc1 - 1);
-            vr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.v + r * key_stride + col));
+            const int r = min(at + j * KPI + kl, kc1 - 1);
+            vr[j] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)((r * key_stride + col) * 2), 0, 2));
         }
     };
     if (base < kc1) load_kv(base);
