@@ -10,7 +10,9 @@
 // Structure.  A block of WGM x WGN waves owns a BM x BN tile of C; each wave a
 // (BM/WGM) x (BN/WGN) sub-tile of 32x32 v_mfma_f32_32x32x16 tiles.
 // K advances in 64-wide stages held in an LDS ring of STAGES slots:
-//  * global -> LDS with global_load_lds_dwordx4: one wave instruction moves
+//  * global -> LDS with direct 16-byte loads (buffer_load_dwordx4 ... lds
+//    through a descriptor over the tile's rows on the large tiles,
+//    global_load_lds_dwordx4 on the others): one wave instruction moves
 //    8 rows x 128 bytes (a 64-element K slice of 8 rows) straight into LDS,
 //    no registers involved, so up to STAGES-1 stages are in flight while the
 //    MFMAs work on the oldest;
