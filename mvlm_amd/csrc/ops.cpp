@@ -306,7 +306,7 @@ int make_gemv(mvlm_device* dev, const mvlm_buffer* x, int x_dtype, const mvlm_we
         const bool streams = M == 1 ? stream_supported(W) : (M <= 4 && stream_supported(W, M));
         if (!streams && !skinny_supported(1, &W, op->num_cus))
             return set_error(MVLM_ERR_UNSUPPORTED, "%s: K=%d is outside the skinny kernel's range (a multiple of 32 "
-                             "whose block scales fit in LDS)", fn, K);
+                             "whose block scales fit in LDS, weight below 2 GiB)", fn, K);
         op->kind = OP_GEMV_QUANT;
         return MVLM_OK;
     }
@@ -339,7 +339,7 @@ int make_gemv_group(mvlm_device* dev, int M, int count, const mvlm_gemv_desc* de
         REQUIRE(d.x_dtype == descs[0].x_dtype, "%s: entry %d x dtype differs from entry 0", fn, i);
         if (M == 1 && !stream_supported(d.W))
             return set_error(MVLM_ERR_UNSUPPORTED, "%s: entry %d: rows of %lld bytes (K=%d) are outside the grouped "
-                             "kernel's range (<= 16 KiB, K a multiple of the 16-byte vector)", fn, i,
+                             "kernel's range (<= 16 KiB, K a multiple of the 16-byte vector, weight below 2 GiB)", fn, i,
                              (long long)weight_row_bytes(d.W), d.W->K);
         if (M > 1 && d.W->K % 32 != 0)
             return set_error(MVLM_ERR_UNSUPPORTED, "%s: entry %d: K=%d is not a multiple of 32", fn, i, d.W->K);
