@@ -621,6 +621,19 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
         rowo[r] = (uint32_t)(row * P.ld_bytes);
         srow[r] = (int)(row * (nb * 2) - s_base);
     }
+    // The epilogue operands of the output this lane stores (lane j < R MX
+    // stores output j), requested before the codes: the store at the end then
+    // takes them from registers instead of waiting for a round trip to memory.
+    constexpr int NV = R * MX;
+    const int jr = (lane & (NV - 1)) / MX, jm = (lane & (NV - 1)) % MX;
+    float eb = 0.0f, em = 1.0f, er = 0.0f;
+    if (P.ep_on) {
+        const int erow = min(row0 + jr, rb1 - 1);
+        const int64_t eidx = MX == 1 ? (int64_t)erow : (int64_t)min(jm, P.M - 1) * P.N + erow;
+        if (P.ep.bias) eb = load_as_f32(P.ep.bias, erow, P.ep.dtype);
+        if (P.ep.mul) em = load_as_f32(P.ep.mul, eidx, P.ep.dtype);
+        if (P.ep.res) er = load_as_f32(P.ep.res, eidx, P.ep.dtype);
+    }
     u32x4 q[R][CW];
     int kk[CW];
     bool valid[CW];
@@ -751,27 +764,32 @@ __device__ __forceinline__ void stream_rows(const StreamProblem& P, int rb0, int
         }
     }
     // the R x MX sums over the wave: lane j < R * MX ends with sum j = r * MX + m
-    constexpr int NV = R * MX;
     float flat[NV];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int m = 0; m < MX; ++m) flat[r * MX + m] = acc[r][m];
     const float tot = wave_sum_lanes<NV>(flat, lane);
-    const int jr = (lane & (NV - 1)) / MX, jm = (lane & (NV - 1)) % MX;
 
-    // y[m][row] (and the epilogue's mul / residual [m][row], bias [row]),
-    // the NV outputs of a wave stored by NV lanes at once
+    // y[m][row] with the epilogue (apply_epilogue's steps in its order, on the
+    // operands loaded above), the NV outputs of a wave stored by NV lanes at once
+    auto epilogue = [&](float v) {
+        if (P.ep.bias) v += eb;
+        if (P.ep.act == 1) v = gelu_tanh(v);
+        else if (P.ep.act == 2) v = silu(v);
+        if (P.ep.mul) v *= em;
+        if (P.ep.res) v += er;
+        return v;
+    };
     auto store_row = [&](int row, int m, float v) {
         if constexpr (ROLE == 1) v = ok ? v : __builtin_nanf("");
+        if (P.ep_on) v = epilogue(v);
         if (MX == 1 && y_device) {   // fp32 y (checked on the host), read by other workgroups of the launch
-            const float out = P.ep_on ? apply_epilogue(P.ep, v, row, row) : v;
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(out), dev_rsrc(P.y, P.N * 4), row * 4, 0, kCpolDevice);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), dev_rsrc(P.y, P.N * 4), row * 4, 0, kCpolDevice);
         } else if constexpr (MX == 1) {
-            store_out(P.y, row, P.ep_on ? apply_epilogue(P.ep, v, row, row) : v, P.y_dtype);
+            store_out(P.y, row, v, P.y_dtype);
         } else {
-            const int64_t idx = (int64_t)m * P.N + row;
-            store_out(P.y, idx, P.ep_on ? apply_epilogue(P.ep, v, idx, row) : v, P.y_dtype);
+            store_out(P.y, (int64_t)m * P.N + row, v, P.y_dtype);
         }
     };
     if constexpr (SPLIT == 1) {
