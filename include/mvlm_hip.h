@@ -180,7 +180,8 @@ int mvlm_gemv_exact(mvlm_device* dev, const mvlm_buffer* x, const mvlm_weight* W
  * formula of activations.cl:68 (the kernel there evaluates the tanh with the
  * sign flipped, activations.cl:96-116, which this library does not reproduce).
  * bias ([N]), mul and residual ([M][N], row stride N) are optional, have the
- * output's dtype, and may alias the output. */
+ * output's dtype, start at a multiple of its size (else MVLM_ERR_INVALID_ARG),
+ * and may alias the output. */
 enum mvlm_activation {
     MVLM_ACT_NONE = 0,
     MVLM_ACT_GELU_TANH = 1,

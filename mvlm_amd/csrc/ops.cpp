@@ -82,16 +82,19 @@ int make_epilogue(mvlm_device* dev, const mvlm_epilogue* in, int M, int N, int c
     if (in->bias) {
         REQUIRE(in->bias->dev == dev, "%s: bias belongs to another device", fn);
         NEED(in->bias, (size_t)N * es, "bias");
+        REQUIRE((uintptr_t)in->bias->ptr % es == 0, "%s: bias does not start at a multiple of %zu bytes", fn, es);
         out->bias = in->bias->ptr;
     }
     if (in->mul) {
         REQUIRE(in->mul->dev == dev, "%s: mul belongs to another device", fn);
         NEED(in->mul, (size_t)M * N * es, "mul");
+        REQUIRE((uintptr_t)in->mul->ptr % es == 0, "%s: mul does not start at a multiple of %zu bytes", fn, es);
         out->mul = in->mul->ptr;
     }
     if (in->residual) {
         REQUIRE(in->residual->dev == dev, "%s: residual belongs to another device", fn);
         NEED(in->residual, (size_t)M * N * es, "residual");
+        REQUIRE((uintptr_t)in->residual->ptr % es == 0, "%s: residual does not start at a multiple of %zu bytes", fn, es);
         out->res = in->residual->ptr;
     }
     out->act = in->activation;

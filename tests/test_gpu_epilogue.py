@@ -247,6 +247,49 @@ def test_plan_epilogues_match_direct_calls(dev, orc):
     plan.destroy()
 
 
+def offset_operands(dev, orc, M, N, dt, seed, offset):
+    """bias, mul and residual as views starting `offset` bytes into their buffers"""
+    ops, vals = make_operands(dev, orc, M, N, dt, seed, True, True, True)
+    es = 4 if dt == F32 else 2
+    views, parents = {}, []
+    for name, n in (("bias", N), ("mul", M * N), ("residual", M * N)):
+        raw = ops[name].download(np.uint8, n * es)
+        parent = dev.upload(np.concatenate([np.full(offset, 0x7F, np.uint8), raw]))
+        parents.append(parent)
+        views[name] = parent.view(offset, n * es)
+    return views, vals, parents
+
+
+@pytest.mark.parametrize("yd", [F16, BF16])
+def test_epilogue_operands_off_word_boundary(dev, orc, yd):
+    """16-bit epilogue operands starting 2 bytes into a 32-bit word, odd N,
+    through the streaming kernel (M = 1) and the MFMA GEMM"""
+    N, K = 515, 1024
+    x = orc.normal_f16(K, 0x81)
+    Wt = orc.normal_f16(N * K, 0x82, 0.05)
+    W = dev.pack(Wt, F16, N, K)
+    W64 = from_storage(orc, Wt, F16).reshape(N, K)
+    ops, vals, keep = offset_operands(dev, orc, 1, N, yd, 0x83, 2)
+    y = dev.alloc(N * 2)
+    dev.gemv_ex(dev.upload(x), F16, W, y, yd, N, K, bias=ops["bias"], act=GELU, mul=ops["mul"],
+                residual=ops["residual"])
+    got = from_storage(orc, y.download(np.uint16, N), yd)[None]
+    Y64, S = orc.gemm_f64(from_storage(orc, x, F16)[None], W64, 1, N, K)
+    check(orc, got, Y64, S, vals, GELU, yd, 1e-5)
+
+    M = 37
+    A = orc.normal_f16(M * K, 0x84)
+    opsm, valsm, keepm = offset_operands(dev, orc, M, N, yd, 0x85, 2)
+    C = dev.alloc(M * N * 2)
+    dev.gemm_packed_ex(dev.upload(A), F16, W, C, yd, M, N, K, bias=opsm["bias"], act=SILU, mul=opsm["mul"],
+                       residual=opsm["residual"])
+    got = from_storage(orc, C.download(np.uint16, M * N), yd).reshape(M, N)
+    Y64, S = orc.gemm_f64(from_storage(orc, A, F16).reshape(M, K), W64, M, N, K)
+    check(orc, got, Y64, S, valsm, SILU, yd, 1e-4)
+    for v in list(ops.values()) + list(opsm.values()):
+        v.free()
+
+
 def test_epilogue_argument_errors(dev, orc):
     N, K = 64, 64
     W = dev.pack(orc.normal_f16(N * K, 1), F16, N, K)
@@ -258,3 +301,9 @@ def test_epilogue_argument_errors(dev, orc):
     with pytest.raises(m.MvlmError) as e:
         dev.gemv_ex(x, F16, W, y, F32, N, K, act=7)
     assert e.value.code == native.ERR_INVALID_ARG
+    odd = dev.alloc(N * 4 + 4)
+    for dt, es, off in ((F16, 2, 1), (F32, 4, 2)):
+        y2 = dev.alloc(N * 4)
+        with pytest.raises(m.MvlmError) as e:
+            dev.gemv_ex(x, F16, W, y2, dt, N, K, residual=odd.view(off, N * es))
+        assert e.value.code == native.ERR_INVALID_ARG and "multiple of" in str(e.value)
